@@ -1,0 +1,246 @@
+#!/usr/bin/env python3
+"""Benchmark of the FP4 dequant-GEMM hot path on one MI355X.
+
+Headline (BASELINE.json metric "FP4 dequant-GEMM: achieved HBM TB/s at M=1;
+TFLOP/s at M=2048"):
+  * value  = achieved HBM TB/s at M=1 over one Llama-3-8B layer (config 2: qkv
+    4096->6144, o 4096->4096, gate_up 4096->28672, down 14336->4096, summed),
+    algorithmic bytes (packed weights + scales + A + C) / GPU time;
+  * prefill = TFLOP/s at M=2048 on 4096->14336 and 14336->4096 (config 4).
+A "step" is one pass of the four layer GEMMs.  Weights are synthetic
+(N(0, 0.02) fp16 quantized on the GPU by the library's FP4 quantizer, g=128),
+with enough rotated copies that every step reads HBM, not the 256 MB
+Infinity Cache.  Kernel time comes from HIP events recorded on the launch
+stream; the launches are queued behind a GPU sleep so host launch overhead is
+not part of the measurement (this is the time a captured decode loop sees).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--all]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "metal-marlin_amd"))
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+FP16_PEAK_TFLOPS = 2500.0      # MI355X dense fp16 MFMA, TFLOP/s
+G = 128
+LLAMA_LAYER = [("qkv", 4096, 6144), ("o", 4096, 4096), ("gate_up", 4096, 28672),
+               ("down", 14336, 4096)]
+PREFILL = [("up", 4096, 14336), ("down", 14336, 4096)]
+ROTATE_BYTES = 640 << 20       # rotated weight footprint > 2.5x the 256 MB MALL
+
+
+def alg_bytes(M: int, K: int, N: int, int4: bool = False) -> int:
+    """Algorithmic HBM bytes of one GEMM: packed B + scales (+ zeros) + A + C."""
+    b = K * N // 2 + 2 * N * (K // G) * (2 if int4 else 1)
+    return b + 2 * M * K + 2 * M * N
+
+
+def make_weights(torch, mmfp4, K: int, N: int, seed: int, int4: bool = False):
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    w = (torch.randn((N, K), generator=gen, device="cuda") * 0.02).half()
+    if int4:
+        return mmfp4.pack_u4_weights(w, group_size=G)
+    return mmfp4.quantize_fp4(w, group_size=G)
+
+
+def gpu_sleep_ahead(torch, ms: float = 60.0) -> None:
+    """Queue a GPU-side wait so the host can enqueue the timed launches ahead."""
+    torch.cuda._sleep(int(ms * 1e-3 * 2.1e9))
+
+
+def timed_launches(torch, launches, steps: int, warmup: int):
+    """Run `launches` (list of per-step lists of callables) warmup + steps
+    times; returns (total_ms over `steps`, per-launch ms list)."""
+    nper = len(launches[0])
+    for s in range(warmup):
+        for fn in launches[s % len(launches)]:
+            fn()
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps * nper + 1)]
+    gpu_sleep_ahead(torch, 20.0 + 0.05 * steps * nper)
+    ev[0].record()
+    i = 1
+    for s in range(steps):
+        for fn in launches[s % len(launches)]:
+            fn()
+            ev[i].record()
+            i += 1
+    torch.cuda.synchronize()
+    per = [ev[j].elapsed_time(ev[j + 1]) for j in range(len(ev) - 1)]
+    return ev[0].elapsed_time(ev[-1]), per
+
+
+def run_layer_bench(torch, mmfp4, M: int, steps: int, warmup: int, int4: bool = False):
+    layer_w = sum(alg_bytes(0, K, N, int4) for _, K, N in LLAMA_LAYER)
+    copies = max(2, -(-ROTATE_BYTES // layer_w))
+    sets = []
+    for c in range(copies):
+        ws = [make_weights(torch, mmfp4, K, N, 100 * c + i, int4)
+              for i, (_, K, N) in enumerate(LLAMA_LAYER)]
+        sets.append(ws)
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    acts = {K: torch.randn((M, K), generator=gen, device="cuda").half() for _, K, _ in LLAMA_LAYER}
+    launches = []
+    for ws in sets:
+        step = []
+        for (_, K, N), wt in zip(LLAMA_LAYER, ws):
+            a = acts[K]
+            if int4:
+                step.append(lambda a=a, w=wt: mmfp4.marlin_gemm_int4(a, w[0], w[1], w[2], G))
+            else:
+                step.append(lambda a=a, w=wt: mmfp4.marlin_gemm_fp4(a, w[0], w[1], G))
+        launches.append(step)
+    total_ms, per = timed_launches(torch, launches, steps, warmup)
+    step_bytes = sum(alg_bytes(M, K, N, int4) for _, K, N in LLAMA_LAYER)
+    per_shape = {}
+    for idx, (name, K, N) in enumerate(LLAMA_LAYER):
+        ts = per[idx::len(LLAMA_LAYER)]
+        us = 1e3 * sum(ts) / len(ts)
+        per_shape[name] = {"K": K, "N": N, "us": round(us, 3),
+                           "GBps": round(alg_bytes(M, K, N, int4) / (us * 1e3), 1)}
+    return {"ms_per_step": total_ms / steps, "step_bytes": step_bytes,
+            "launch_us_avg": 1e3 * sum(per) / len(per), "per_shape": per_shape,
+            "copies": copies}
+
+
+def run_prefill_bench(torch, mmfp4, M: int, steps: int, warmup: int):
+    ws = [make_weights(torch, mmfp4, K, N, 7 + i) for i, (_, K, N) in enumerate(PREFILL)]
+    gen = torch.Generator(device="cuda").manual_seed(2)
+    acts = {K: torch.randn((M, K), generator=gen, device="cuda").half() for _, K, _ in PREFILL}
+    step = [lambda a=acts[K], w=w: mmfp4.marlin_gemm_fp4(a, w[0], w[1], G)
+            for (_, K, _), w in zip(PREFILL, ws)]
+    total_ms, per = timed_launches(torch, [step], steps, warmup)
+    flops = sum(2 * M * K * N for _, K, N in PREFILL)
+    per_shape = {}
+    for idx, (name, K, N) in enumerate(PREFILL):
+        ts = per[idx::len(PREFILL)]
+        us = 1e3 * sum(ts) / len(ts)
+        per_shape[name] = {"K": K, "N": N, "us": round(us, 2),
+                           "TFLOPs": round(2 * M * K * N / (us * 1e-6) / 1e12, 1)}
+    return {"ms_per_step": total_ms / steps, "flops": flops, "per_shape": per_shape,
+            "launch_us_avg": 1e3 * sum(per) / len(per)}
+
+
+def cpu_baseline(budget_s: float = 15.0):
+    """The reference's CPU path (torch fp32 LUT dequant + matmul, redone per
+    call) over the same Llama layer at M=1, on this host's cores."""
+    import numpy as np
+    import torch
+    sys.path.insert(0, str(ROOT))
+    from oracle.cpu_path import marlin_gemm_fp4_cpu
+    from oracle.fp4 import quantize_fp4
+    cores = os.cpu_count() or 1
+    torch.set_num_threads(cores)
+    rng = np.random.default_rng(0)
+    mats = []
+    for _, K, N in LLAMA_LAYER:
+        # random codes/scales of the right shape (quantizing 112 M weights on
+        # the host would dominate the budget); the CPU path's cost does not
+        # depend on the values.
+        packed = torch.from_numpy(rng.integers(0, 2**32, (K // 8, N), dtype=np.uint64)
+                                  .astype(np.uint32).view(np.int32))
+        scales = torch.from_numpy(rng.normal(0, 0.005, (K // G, N)).astype(np.float16))
+        mats.append((torch.randn(1, K).half(), packed, scales))
+    del quantize_fp4
+    marlin_gemm_fp4_cpu(*mats[1], G)          # warm-up on the smallest shape
+    t0 = time.perf_counter()
+    steps = 0
+    while True:
+        for a, p, s in mats:
+            marlin_gemm_fp4_cpu(a, p, s, G)
+        steps += 1
+        if time.perf_counter() - t0 > budget_s or steps >= 10:
+            break
+    dt = (time.perf_counter() - t0) / steps
+    step_bytes = sum(alg_bytes(1, K, N) for _, K, N in LLAMA_LAYER)
+    return {"value": round(step_bytes / dt / 1e12, 6), "unit": "TB/s", "cores": cores,
+            "kind": "port", "ms_per_step": round(dt * 1e3, 1),
+            "sample": f"{steps} step(s) of the 4-GEMM Llama-3-8B layer at M=1 "
+                      f"(torch-CPU fp32 dequant+matmul, {platform.processor() or 'host'})"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--all", action="store_true", help="also report configs 1, 3, 5 and M=8/32")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU only: the FP4 dequant-GEMM "
+                          "path is single-GPU by design (see DESIGN.md for how it would "
+                          "shard); run with --gpus 1"}))
+        return 2
+
+    import torch
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no ROCm device visible"}))
+        return 1
+    import mmfp4
+
+    torch.cuda.synchronize()
+    layer = run_layer_bench(torch, mmfp4, 1, args.steps, args.warmup)
+    pre = run_prefill_bench(torch, mmfp4, 2048, max(5, args.steps // 20), max(2, args.warmup // 10))
+    value_tbs = layer["step_bytes"] / (layer["ms_per_step"] * 1e-3) / 1e12
+    achieved = layer["step_bytes"] / 4 / (layer["launch_us_avg"] * 1e-6) / 1e9
+    tflops = pre["flops"] / (pre["ms_per_step"] * 1e-3) / 1e12
+    out = {
+        "metric": "FP4 dequant-GEMM: achieved HBM TB/s at M=1; TFLOP/s at M=2048",
+        "value": round(value_tbs, 4),
+        "unit": "TB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(layer["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp4(e2m1,g128) x fp16 -> fp32 acc",
+        "data": "synthetic: weights N(0,0.02) fp16 quantized by the library's FP4 quantizer "
+                "(g=128), activations N(0,1) fp16, seeded",
+        "config": {"workload": "llama3-8b-layer-fp4-decode-M1", "M": 1, "group_size": G,
+                   "layers": {n: [K, N] for n, K, N in LLAMA_LAYER},
+                   "weight_copies_rotated": layer["copies"]},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": None, "kernel": "k_skinny (M<=32 decode path)",
+                     "launch_us_avg": round(layer["launch_us_avg"], 3)},
+        "per_shape_m1": layer["per_shape"],
+        "prefill_m2048": {"tflops": round(tflops, 1), "frac_fp16_peak": round(tflops /
+                          FP16_PEAK_TFLOPS, 4), "ms_per_step": round(pre["ms_per_step"], 4),
+                          "per_shape": pre["per_shape"], "kernel": "k_prefill (MFMA 32x32x16)"},
+    }
+    if args.all:
+        extra = {}
+        for M in (8, 32):
+            r = run_layer_bench(torch, mmfp4, M, max(20, args.steps // 4), 5)
+            extra[f"fp4_layer_M{M}"] = {"TBps": round(r["step_bytes"] / (r["ms_per_step"] * 1e-3)
+                                                      / 1e12, 3), "per_shape": r["per_shape"]}
+        for M in (1, 16):
+            r = run_layer_bench(torch, mmfp4, M, max(20, args.steps // 4), 5, int4=True)
+            extra[f"int4_layer_M{M}"] = {"TBps": round(r["step_bytes"] / (r["ms_per_step"] * 1e-3)
+                                                       / 1e12, 3), "per_shape": r["per_shape"]}
+        for M in (512, 8192):
+            r = run_prefill_bench(torch, mmfp4, M, 5, 2)
+            extra[f"prefill_M{M}"] = {"TFLOPs": round(r["flops"] / (r["ms_per_step"] * 1e-3)
+                                                      / 1e12, 1), "per_shape": r["per_shape"]}
+        out["extra"] = extra
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(out))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

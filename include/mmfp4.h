@@ -1,0 +1,117 @@
+/*
+ * mmfp4.h -- C ABI of libmmfp4.so, the gfx950 (MI355X) FP4-E2M1 / INT4
+ * dequant-GEMM library and its MoE grouped-expert variant.
+ *
+ * Every entry point is asynchronous on the caller's HIP stream (`stream` is a
+ * hipStream_t passed as void*; NULL = the default stream) and returns 0 on
+ * success, 1 for an invalid argument, 2 for a launch failure; the message is
+ * then available from mm_last_error() (thread-local).  Pointers are device
+ * pointers; fp16 data is passed as uint16_t bit patterns.
+ *
+ * Data layout is the reference's "Marlin" layout:
+ *   B       uint32 [K/8, N]   word (kp, n) holds rows k = 8kp+i in bits 4i..4i+3
+ *   scales  fp16   [K/g, N]   (g = group_size along K)
+ *   zeros   fp16   [K/g, N]   (INT4 only)
+ *   A       fp16   [M, K] row-major, C fp16 [M, N] row-major
+ */
+#ifndef MMFP4_H
+#define MMFP4_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* mm_last_error(void);
+
+/* ---------------------------------------------------------------- dequant */
+
+/* W[K,N] fp16 = fp16_RNE(E2M1[code] * scale), non-finite -> +0.
+ * Replaces metal_marlin/kernels_core.py:2079-2133 (dequant_fp4, inline kernel
+ * :747-791) and metal_marlin/metal_marlin.py:580-612 (dequant_fp4_bulk). */
+int mm_fp4_dequant(const uint32_t* B, const uint16_t* scales, uint16_t* W, int K, int N,
+                   int group_size, void* stream);
+
+/* W[K,N] fp16 = fp16_RNE(fp16(q - clamp(z, +-127)) * s), non-finite -> +0.
+ * Replaces metal_marlin/metal_marlin.py:615-678 (dequant_int4_bulk) and
+ * :283-348 (unpack_u4_weights), kernel src/marlin_gemm.metal:1984-2012. */
+int mm_u4_dequant(const uint32_t* B, const uint16_t* scales, const uint16_t* zeros, uint16_t* W,
+                  int K, int N, int group_size, void* stream);
+
+/* ---------------------------------------------------------------- quantize */
+
+/* FP4 E2M1 quantizer from W[N,K] (fp16, or fp32 when w_is_f32 != 0) into
+ * B[K/8,N] + scales[K/g,N].  Replaces metal_marlin/quantize_fp4.py:131-284
+ * (quantize_fp4, weight-only path). */
+int mm_fp4_quantize(const void* W, int w_is_f32, int N, int K, int group_size, uint32_t* B,
+                    uint16_t* scales, void* stream);
+
+/* Asymmetric INT4 quantizer from W[N,K] fp16 into B, scales, zeros.
+ * Replaces metal_marlin/metal_marlin.py:184-280 (pack_u4_weights). */
+int mm_u4_quantize(const uint16_t* W, int N, int K, int group_size, uint32_t* B,
+                   uint16_t* scales, uint16_t* zeros, void* stream);
+
+/* ------------------------------------------------------------------- GEMM */
+
+/* Bytes of workspace mm_fp4_gemm / mm_u4_gemm need for this shape.  The
+ * workspace starts with split-K arrival counters that must be zero before the
+ * first use; every call leaves them at zero again, so one workspace can be
+ * reused by consecutive calls on the same stream (not by concurrent calls). */
+size_t mm_gemm_workspace_bytes(int M, int N, int K);
+
+/* C[M,N] = A[M,K] . dequant_fp4(B, scales), fp32 accumulation, fp16 out.
+ * Replaces metal_marlin/kernels_core.py:1830-1937 (marlin_gemm_fp4),
+ * metal_marlin/metal_dispatch.py:4045-4181 (dispatch_gemm_fp4), :3914-4042
+ * (_dispatch_decode_gemv_fp4), :1791-1861 (MetalKernelLibrary.fp4_gemm) and
+ * the native FFI metal_marlin/cpp_extension.cpp:502-527 (_cpp_ext.mmfp4_gemm).
+ * Requires K % 8 == 0, N % 4 == 0, group_size % 8 == 0, K % group_size == 0;
+ * A, B 16-byte aligned; scales, C 8-byte aligned. */
+int mm_fp4_gemm(const uint16_t* A, const uint32_t* B, const uint16_t* scales, uint16_t* C, int M,
+                int N, int K, int group_size, void* ws, size_t ws_bytes, void* stream);
+
+/* INT4 asymmetric counterpart.  Replaces metal_marlin/kernels_core.py:1959-2066
+ * (marlin_gemm_int4) and metal_marlin/metal_dispatch.py:1863-1937
+ * (MetalKernelLibrary.int4_gemm). */
+int mm_u4_gemm(const uint16_t* A, const uint32_t* B, const uint16_t* scales,
+               const uint16_t* zeros, uint16_t* C, int M, int N, int K, int group_size, void* ws,
+               size_t ws_bytes, void* stream);
+
+/* -------------------------------------------------------------------- MoE */
+
+/* Stable counting sort of the T*k (token, slot) assignments by expert.
+ * expert_ids int32 [T, k]; outputs offsets int32 [E+1], sorted_idx int32 [T*k]
+ * (flat index t*k+slot, ascending within an expert) and inverse int32 [T*k].
+ * Replaces metal_marlin/moe_dispatch.py:493-555 (group_tokens_by_expert),
+ * :726-786 (group_tokens_by_expert_full) and the Metal moe_gpu_sort
+ * (src/moe_dispatch.metal:1600-1626).  Requires E <= 1024. */
+int mm_moe_sort(const int32_t* expert_ids, int T, int k, int E, int32_t* offsets,
+                int32_t* sorted_idx, int32_t* inverse, void* stream);
+
+/* Grouped expert GEMM over expert-sorted rows.  For expert e, rows
+ * r in [offsets[e], offsets[e+1]) compute Y[r] = X[row(r)] . dequant(B[e], S[e]),
+ * where row(r) = sorted_idx[r] / k when gather != 0 (rows of X are tokens)
+ * and row(r) = r otherwise (X already in sorted order).  B: uint32 [E, K/8, N],
+ * S: fp16 [E, K/g, N].  act = 0: Y is [T*k, N];  act = 1 (SwiGLU): the first
+ * N/2 columns are gate and the last N/2 up, Y[r, j] = silu(gate_j) * up_j is
+ * [T*k, N/2].  Replaces metal_marlin/kernels/moe.py:583-727
+ * (moe_expert_gemm_fp4, kernel src/moe_expert_gemm.metal:557-782) and the
+ * expert MLP of metal_marlin/moe_dispatch.py:1241-1431 (_fused_expert_mlp). */
+int mm_moe_grouped_gemm(const uint16_t* X, const int32_t* sorted_idx, const int32_t* offsets,
+                        int gather, int k, int T, const uint32_t* B, const uint16_t* S, int E,
+                        int K, int N, int group_size, int act, uint16_t* Y, void* stream);
+
+/* out[t, :] = sum_{j<k} probs[t, j] * Y[inverse[t*k + j], :] in fp32 (fixed
+ * slot order, deterministic), written as fp16 [T, H].  Replaces
+ * metal_marlin/moe_dispatch.py:812-925 (scatter_expert_outputs /
+ * _aggregate_expert_outputs). */
+int mm_moe_combine(const uint16_t* Y, const float* probs, const int32_t* inverse, int T, int k,
+                   int H, uint16_t* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MMFP4_H */

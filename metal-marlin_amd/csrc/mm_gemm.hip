@@ -1,0 +1,372 @@
+// Fused FP4 (E2M1) / INT4 dequant-GEMM for gfx950:  C[M,N] = A[M,K] . dequant(B, S[, Z])
+//
+// Reference path: metal_marlin/kernels_core.py:1830-1937 (marlin_gemm_fp4),
+// :1959-2066 (marlin_gemm_int4), metal_dispatch.py:4045-4181 (dispatch_gemm_fp4)
+// and the Metal kernels src/marlin_gemm.metal:938-1150, 2053-2532,
+// src/decode_gemv.metal:204-266.  Numerics: each weight is dequantised to the
+// reference's fp16 value (mm_common.h), products accumulate in fp32 on the
+// matrix cores, and the result is rounded once to fp16.
+//
+// Two kernels:
+//  * skinny (M <= 32, decode): weights stream HBM -> registers -> MFMA with no
+//    LDS staging; the M rows ride in a 16-row MFMA operand (zero padded).  A
+//    block holds NW waves that split its K range; the block reduces the waves
+//    in LDS, and a K split across blocks is reduced by the last-arriving block
+//    (deterministic order, counter left at zero for the next call).
+//  * prefill (M > 32): 32x32x16 MFMA tiles, A double-buffered through LDS,
+//    B loaded as packed words one chunk ahead and dequantised in registers.
+#include "mm_common.h"
+#include "mm_skinny.h"
+
+// ===========================================================================
+// Skinny path
+// ===========================================================================
+namespace {
+using namespace mmsk;
+
+// Dense skinny kernel.  grid = (ceil(N / (NT*64)), ksplit).
+template <bool INT4, int MT, int NT, int SPW, int NW>
+__global__ void __launch_bounds__(NW * 64)
+k_skinny(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
+         const f16* __restrict__ S, const f16* __restrict__ Z, f16* __restrict__ C, int ldc,
+         int M, int N, int K, int g, int nrounds, float* __restrict__ part,
+         uint32_t* __restrict__ counters) {
+  constexpr int RED = (NW / 2 > 0 ? NW / 2 : 1) * MT * NT * 16 * 64;
+  __shared__ float red[RED];
+  __shared__ uint32_t s_last;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c = lane & 15, q = lane >> 4;
+  const int n0 = blockIdx.x * NT * SK_COLS;
+  const int ksplit = gridDim.y;
+  // Steps owned by this block: NW*SPW*nrounds consecutive 32-k steps; waves
+  // take interleaved SPW-step slabs so each round reads adjacent word rows.
+  const int blk_st0 = blockIdx.y * NW * SPW * nrounds;
+  f32x4 acc[MT][NT][4];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[mt][t][j] = f32x4{0, 0, 0, 0};
+
+  skinny_wave<INT4, MT, NT, SPW>(A, lda, nullptr, 1, M, B, S, Z, N, K, g, n0, SK_COLS,
+                                 blk_st0 + wave * SPW, nrounds, NW * SPW, acc);
+  skinny_block_reduce<MT, NT, NW>(red, acc);
+
+  // Lane (c, q) of wave 0 holds rows 16*mt + 4*q + rr, columns n0 + 64*t + 4*c + j.
+  if (ksplit == 1) {
+    if (wave != 0) return;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const int col = n0 + t * SK_COLS + 4 * c;
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const int row = mt * 16 + 4 * q + rr;
+          if (row < M && col < N)
+            *(f16x4*)(C + (size_t)row * ldc + col) =
+                f16x4{(f16)acc[mt][t][0][rr], (f16)acc[mt][t][1][rr], (f16)acc[mt][t][2][rr],
+                      (f16)acc[mt][t][3][rr]};
+        }
+      }
+    return;
+  }
+  // K split across blocks: publish this block's partial tile, then the last
+  // block of the column tile sums all partials in split order.  Partials and
+  // the counter are accessed with agent-scope atomics (coherent across the
+  // XCDs' L2s without writing back whole caches); a workgroup-scope release
+  // (wait for this wave's stores) orders the stores before the counter bump.
+  if (wave == 0) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const int col = n0 + t * SK_COLS + 4 * c;
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const int row = mt * 16 + 4 * q + rr;
+          if (row < M && col < N) {
+            float* dst = part + ((size_t)blockIdx.y * M + row) * N + col;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              __hip_atomic_store(dst + j, acc[mt][t][j][rr], __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+          }
+        }
+      }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t prev = __hip_atomic_fetch_add(&counters[blockIdx.x], 1u, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+    s_last = (prev == (uint32_t)ksplit - 1u) ? 1u : 0u;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  // Every thread of the last block sums a share of the (row, 4-column) items.
+  constexpr int COLS = NT * SK_COLS;
+  const int nitems = MT * 16 * (COLS / 4);
+  for (int e = threadIdx.x; e < nitems; e += NW * 64) {
+    const int row = e / (COLS / 4), col = n0 + 4 * (e % (COLS / 4));
+    if (row < M && col < N) {
+      float v[4] = {0, 0, 0, 0};
+      for (int y = 0; y < ksplit; ++y) {
+        const float* src = part + ((size_t)y * M + row) * N + col;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          v[j] += __hip_atomic_load(src + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      *(f16x4*)(C + (size_t)row * ldc + col) = f16x4{(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
+    }
+  }
+  if (threadIdx.x == 0)
+    __hip_atomic_store(&counters[blockIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ===========================================================================
+// Prefill path
+// ===========================================================================
+constexpr int PF_BK = 64;             // k per LDS chunk (4 MFMA k-steps of 16)
+constexpr int PF_LDS_STRIDE = PF_BK + 8;  // halves; +16 B per row breaks bank aliasing
+
+template <bool INT4, int WM, int WN, int RB>
+__global__ void __launch_bounds__(WM * WN * 64)
+k_prefill(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
+          const f16* __restrict__ S, const f16* __restrict__ Z, f16* __restrict__ C, int ldc,
+          int M, int N, int K, int g) {
+  constexpr int NTHR = WM * WN * 64;
+  constexpr int BM = WM * 32 * RB;
+  constexpr int BN = WN * 128;
+  constexpr int AVEC = BM * (PF_BK / 8);        // 16-byte A vectors per chunk
+  static_assert(AVEC % NTHR == 0, "A chunk must split evenly over the block");
+  constexpr int AV_PER_THR = AVEC / NTHR;
+  __shared__ f16 As[2][BM * PF_LDS_STRIDE];
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int l32 = lane & 31, h = lane >> 5;
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  const int KP = K >> 3;
+  const int nch = (K + PF_BK - 1) / PF_BK;
+  const int ncol = n0 + wn * 128 + 4 * l32;
+  const bool nok = ncol < N;
+
+  f32x16 acc[RB][4];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[rb][j][v] = 0.0f;
+
+  f16x8 areg[AV_PER_THR];
+  u32x4 bcur[4], bnext[4];
+  f16x4 scur[4], snext[4], zcur[4], znext[4];
+
+  auto load_a = [&](int ch) {
+#pragma unroll
+    for (int i = 0; i < AV_PER_THR; ++i) {
+      const int v = threadIdx.x + i * NTHR;
+      const int row = v / (PF_BK / 8), c8 = v % (PF_BK / 8);
+      const int m = m0 + row, k = ch * PF_BK + c8 * 8;
+      areg[i] = (m < M && k < K) ? *(const f16x8*)(A + (size_t)m * lda + k)
+                                 : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+    }
+  };
+  auto store_a = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < AV_PER_THR; ++i) {
+      const int v = threadIdx.x + i * NTHR;
+      const int row = v / (PF_BK / 8), c8 = v % (PF_BK / 8);
+      *(f16x8*)(&As[buf][row * PF_LDS_STRIDE + c8 * 8]) = areg[i];
+    }
+  };
+  auto load_b = [&](int ch, u32x4 (&w)[4], f16x4 (&s)[4], f16x4 (&z)[4]) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int kp = ch * (PF_BK / 8) + 2 * t + h;
+      const bool ok = nok && kp < KP;
+      const int gi = (kp * 8) / g;
+      w[t] = ok ? *(const u32x4*)(B + (size_t)kp * N + ncol) : u32x4{0, 0, 0, 0};
+      s[t] = ok ? *(const f16x4*)(S + (size_t)gi * N + ncol) : f16x4{0, 0, 0, 0};
+      if constexpr (INT4)
+        z[t] = ok ? *(const f16x4*)(Z + (size_t)gi * N + ncol) : f16x4{0, 0, 0, 0};
+    }
+  };
+
+  load_a(0);
+  store_a(0);
+  load_b(0, bcur, scur, zcur);
+
+  for (int ch = 0; ch < nch; ++ch) {
+    const int buf = ch & 1;
+    const bool more = ch + 1 < nch;
+    if (more) {
+      load_a(ch + 1);
+      load_b(ch + 1, bnext, snext, znext);
+    }
+    __syncthreads();
+    const f16* as = &As[buf][(wm * 32 * RB + l32) * PF_LDS_STRIDE + 8 * h];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      f16x8 af[RB];
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+        af[rb] = *(const f16x8*)(as + rb * 32 * PF_LDS_STRIDE + 16 * t);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        f16 nz = 0;
+        if constexpr (INT4) nz = -clamp_zero(zcur[t][j]);
+        const f16x8 b = WordDq<INT4>::run(bcur[t][j], sanitize_scale(scur[t][j]), nz);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+          acc[rb][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[rb], b, acc[rb][j], 0, 0, 0);
+      }
+    }
+    if (more) {
+      store_a(buf ^ 1);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        bcur[t] = bnext[t];
+        scur[t] = snext[t];
+        if constexpr (INT4) zcur[t] = znext[t];
+      }
+    }
+  }
+
+  // Epilogue: lane holds column 4*l32 + j of tile j, rows 8*(v/4) + 4*h + v%4.
+  if (!nok) return;
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int row = m0 + wm * 32 * RB + rb * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+      if (row < M)
+        *(f16x4*)(C + (size_t)row * ldc + ncol) =
+            f16x4{(f16)acc[rb][0][v], (f16)acc[rb][1][v], (f16)acc[rb][2][v], (f16)acc[rb][3][v]};
+    }
+  }
+}
+
+// ===========================================================================
+// Host-side planning
+// ===========================================================================
+constexpr int SK_NW = 4;
+constexpr int SK_SPW = 4;
+constexpr int SK_NT = 2;
+
+struct SkinnyPlan {
+  int ksplit;
+  int nrounds;
+  int ntiles;
+};
+
+SkinnyPlan plan_skinny(int M, int N, int K) {
+  SkinnyPlan p;
+  const int nsteps = (K / 8 + 3) / 4;                  // 32-k steps
+  const int slab = SK_NW * SK_SPW;                     // steps per block round
+  const int blocks_k = mm_cdiv(nsteps, slab);          // block-rounds along K
+  p.ntiles = mm_cdiv(N, SK_NT * SK_COLS);
+  // Aim for ~1024 blocks; a round is the minimum work of a block.  Larger M
+  // means more partial-sum traffic per split, so split less.
+  const int target = M <= 16 ? 1024 : 512;
+  int ks = mm_cdiv(target, p.ntiles);
+  if (ks > blocks_k) ks = blocks_k;
+  if (ks < 1) ks = 1;
+  p.nrounds = mm_cdiv(blocks_k, ks);
+  p.ksplit = mm_cdiv(blocks_k, p.nrounds);
+  return p;
+}
+
+// The workspace starts with a fixed, shape-independent block of split-K
+// arrival counters (one per column tile); partial sums follow it.
+constexpr int SK_MAX_TILES = 16384;
+constexpr size_t SK_COUNTER_BYTES = (size_t)SK_MAX_TILES * sizeof(uint32_t);
+
+size_t skinny_ws_bytes(int M, int N, int K) {
+  const SkinnyPlan p = plan_skinny(M, N, K);
+  if (p.ksplit == 1) return SK_COUNTER_BYTES;
+  return SK_COUNTER_BYTES + (size_t)p.ksplit * M * N * sizeof(float);
+}
+
+template <bool INT4, int MT>
+int launch_skinny(const f16* A, int lda, const uint32_t* B, const f16* S, const f16* Z, f16* C,
+                  int ldc, int M, int N, int K, int g, void* ws, size_t ws_bytes,
+                  hipStream_t st) {
+  const SkinnyPlan p = plan_skinny(M, N, K);
+  MM_CHECK_ARG(p.ntiles <= SK_MAX_TILES, "gemm: N=%d exceeds the supported %d columns", N,
+               SK_MAX_TILES * SK_NT * SK_COLS);
+  uint32_t* counters = (uint32_t*)ws;
+  float* part = nullptr;
+  if (p.ksplit > 1) {
+    const size_t need = skinny_ws_bytes(M, N, K);
+    MM_CHECK_ARG(ws != nullptr && ws_bytes >= need,
+                 "gemm: workspace of %zu bytes is smaller than the %zu required", ws_bytes, need);
+    part = (float*)((char*)ws + SK_COUNTER_BYTES);
+  }
+  dim3 grid(p.ntiles, p.ksplit);
+  hipLaunchKernelGGL((k_skinny<INT4, MT, SK_NT, SK_SPW, SK_NW>), grid, dim3(SK_NW * 64), 0, st, A,
+                     lda, B, S, Z, C, ldc, M, N, K, g, p.nrounds, part, counters);
+  MM_CHECK_LAUNCH("gemm(skinny)");
+  return 0;
+}
+
+template <bool INT4, int WM, int WN, int RB>
+int launch_prefill(const f16* A, int lda, const uint32_t* B, const f16* S, const f16* Z, f16* C,
+                   int ldc, int M, int N, int K, int g, hipStream_t st) {
+  constexpr int BM = WM * 32 * RB, BN = WN * 128;
+  dim3 grid(mm_cdiv(N, BN), mm_cdiv(M, BM));
+  hipLaunchKernelGGL((k_prefill<INT4, WM, WN, RB>), grid, dim3(WM * WN * 64), 0, st, A, lda, B, S,
+                     Z, C, ldc, M, N, K, g);
+  MM_CHECK_LAUNCH("gemm(prefill)");
+  return 0;
+}
+
+template <bool INT4>
+int gemm_dispatch(const char* who, const f16* A, const uint32_t* B, const f16* S, const f16* Z,
+                  f16* C, int M, int N, int K, int g, void* ws, size_t ws_bytes,
+                  hipStream_t st) {
+  MM_CHECK_ARG(M >= 0 && N > 0 && K > 0, "%s: bad shape M=%d N=%d K=%d", who, M, N, K);
+  MM_CHECK_ARG(K % 8 == 0, "%s: K=%d must be divisible by 8", who, K);
+  MM_CHECK_ARG(N % 4 == 0, "%s: N=%d must be divisible by 4", who, N);
+  MM_CHECK_ARG(g > 0 && g % 8 == 0 && K % g == 0,
+               "%s: group_size=%d must be a multiple of 8 dividing K=%d", who, g, K);
+  MM_CHECK_ARG(((uintptr_t)A & 15) == 0 && ((uintptr_t)B & 15) == 0 && ((uintptr_t)S & 7) == 0 &&
+                   ((uintptr_t)C & 7) == 0 && (!INT4 || ((uintptr_t)Z & 7) == 0),
+               "%s: operands must be 16-byte (A, B) / 8-byte (scales, zeros, C) aligned", who);
+  if (M == 0) return 0;
+  if (M <= 16) return launch_skinny<INT4, 1>(A, K, B, S, Z, C, N, M, N, K, g, ws, ws_bytes, st);
+  if (M <= 32) return launch_skinny<INT4, 2>(A, K, B, S, Z, C, N, M, N, K, g, ws, ws_bytes, st);
+  // Prefill tiles: the largest tile that still gives about one block per CU.
+  const long t256 = (long)mm_cdiv(M, 256) * mm_cdiv(N, 256);
+  if (M > 128 && t256 >= 240)
+    return launch_prefill<INT4, 2, 2, 4>(A, K, B, S, Z, C, N, M, N, K, g, st);
+  if (M > 64) return launch_prefill<INT4, 2, 2, 2>(A, K, B, S, Z, C, N, M, N, K, g, st);
+  return launch_prefill<INT4, 1, 2, 2>(A, K, B, S, Z, C, N, M, N, K, g, st);
+}
+
+}  // namespace
+
+// ===========================================================================
+// C ABI
+// ===========================================================================
+extern "C" size_t mm_gemm_workspace_bytes(int M, int N, int K) {
+  if (M <= 0 || N <= 0 || K <= 0 || M > 32) return SK_COUNTER_BYTES;
+  return skinny_ws_bytes(M, N, K);
+}
+
+extern "C" int mm_fp4_gemm(const uint16_t* A, const uint32_t* B, const uint16_t* S, uint16_t* C,
+                           int M, int N, int K, int g, void* ws, size_t ws_bytes, void* stream) {
+  return gemm_dispatch<false>("mm_fp4_gemm", (const f16*)A, B, (const f16*)S, nullptr, (f16*)C, M,
+                              N, K, g, ws, ws_bytes, (hipStream_t)stream);
+}
+
+extern "C" int mm_u4_gemm(const uint16_t* A, const uint32_t* B, const uint16_t* S,
+                          const uint16_t* Z, uint16_t* C, int M, int N, int K, int g, void* ws,
+                          size_t ws_bytes, void* stream) {
+  return gemm_dispatch<true>("mm_u4_gemm", (const f16*)A, B, (const f16*)S, (const f16*)Z,
+                             (f16*)C, M, N, K, g, ws, ws_bytes, (hipStream_t)stream);
+}

@@ -1,0 +1,248 @@
+// MoE grouped-expert FP4 path for gfx950: device counting sort of the
+// (token, slot) assignments, a grouped expert GEMM over the expert-sorted rows
+// (optionally gathering token rows and applying SwiGLU in the epilogue), and
+// a deterministic probability-weighted combine.
+//
+// Reference: metal_marlin/moe_dispatch.py:493-555 (group_tokens_by_expert),
+// :789-809 (gather_for_experts), :812-925 (scatter/aggregate),
+// :1241-1431 (_fused_expert_mlp); metal_marlin/kernels/moe.py:583-727
+// (moe_expert_gemm_fp4); Metal src/moe_expert_gemm.metal:557-782.  The
+// reference's grouped kernel accumulates out[token] += p*y with a
+// non-atomic read-modify-write; here every output row is owned by exactly one
+// writer and the combine sums the k slots in fixed order.
+#include "mm_common.h"
+#include "mm_skinny.h"
+
+namespace {
+using namespace mmsk;
+
+constexpr int SORT_THREADS = 1024;
+constexpr int SORT_WAVES = SORT_THREADS / 64;
+
+// One block.  Dynamic LDS: cursor[E] + wcnt[SORT_WAVES][E] ints.
+__global__ void __launch_bounds__(SORT_THREADS)
+k_moe_sort(const int32_t* __restrict__ ids, int n, int E, int32_t* __restrict__ offsets,
+           int32_t* __restrict__ sorted_idx, int32_t* __restrict__ inverse) {
+  extern __shared__ int lds[];
+  int* cursor = lds;            // [E]
+  int* wcnt = lds + E;          // [SORT_WAVES][E]
+  __shared__ int scan[SORT_THREADS];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+  for (int e = tid; e < E; e += SORT_THREADS) cursor[e] = 0;
+  __syncthreads();
+  for (int i = tid; i < n; i += SORT_THREADS) {
+    const int e = ids[i];
+    if (e >= 0 && e < E) atomicAdd(&cursor[e], 1);
+  }
+  __syncthreads();
+  // Exclusive scan of the per-expert counts (E <= SORT_THREADS).
+  const int mine = tid < E ? cursor[tid] : 0;
+  scan[tid] = mine;
+  __syncthreads();
+  for (int d = 1; d < SORT_THREADS; d <<= 1) {
+    const int v = tid >= d ? scan[tid - d] : 0;
+    __syncthreads();
+    scan[tid] += v;
+    __syncthreads();
+  }
+  if (tid < E) {
+    const int excl = scan[tid] - mine;
+    cursor[tid] = excl;
+    offsets[tid] = excl;
+  }
+  if (tid == 0) offsets[E] = scan[SORT_THREADS - 1];
+  __syncthreads();
+
+  // Stable placement, 1024 assignments per pass.  Within a wave the rank of an
+  // assignment among equal experts comes from a ballot over the lanes below it;
+  // across waves from a per-expert prefix of the waves' counts.
+  for (int base = 0; base < n; base += SORT_THREADS) {
+    for (int x = tid; x < SORT_WAVES * E; x += SORT_THREADS) wcnt[x] = 0;
+    __syncthreads();
+    const int i = base + tid;
+    const int e = (i < n) ? ids[i] : -1;
+    const bool valid = e >= 0 && e < E;
+    uint64_t pending = __ballot(valid);
+    int rank = 0;
+    const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    while (pending) {
+      const int leader = __ffsll((unsigned long long)pending) - 1;
+      const int le = __shfl(e, leader);
+      const uint64_t same = __ballot(valid && e == le);
+      if (valid && e == le) rank = __popcll(same & below);
+      if (lane == leader) wcnt[wave * E + le] = __popcll(same);
+      pending &= ~same;
+    }
+    __syncthreads();
+    for (int x = tid; x < E; x += SORT_THREADS) {
+      int run = cursor[x];
+      for (int w = 0; w < SORT_WAVES; ++w) {
+        const int c = wcnt[w * E + x];
+        wcnt[w * E + x] = run;
+        run += c;
+      }
+      cursor[x] = run;
+    }
+    __syncthreads();
+    if (valid) {
+      const int pos = wcnt[wave * E + e] + rank;
+      sorted_idx[pos] = i;
+      inverse[i] = pos;
+    }
+    __syncthreads();
+  }
+}
+
+// Grouped expert GEMM.  grid = (column tiles, 1, E); block = NW waves which
+// split K; the block walks its expert's rows in chunks of MT*16.
+//   act == 0: NT=2 tiles of 64 columns at n0 and n0+64.
+//   act == 1: tile 0 = gate columns [n0, n0+64), tile 1 = up columns
+//             [N/2 + n0, ...); output silu(gate) * up, width N/2.
+constexpr int MOE_NW = 4;
+constexpr int MOE_SPW = 4;
+
+template <int MT>
+__global__ void __launch_bounds__(MOE_NW * 64)
+k_moe_grouped(const f16* __restrict__ X, const int32_t* __restrict__ sorted_idx,
+              const int32_t* __restrict__ offsets, int gather, int topk,
+              const uint32_t* __restrict__ Ball, const f16* __restrict__ Sall, int K, int N,
+              int g, int act, f16* __restrict__ Y) {
+  constexpr int NT = 2;
+  __shared__ float red[(MOE_NW / 2) * MT * NT * 16 * 64];
+  const int e = blockIdx.z;
+  const int r0 = offsets[e], r1 = offsets[e + 1];
+  if (r1 <= r0) return;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c = lane & 15, q = lane >> 4;
+  const uint32_t* B = Ball + (size_t)e * (K / 8) * N;
+  const f16* S = Sall + (size_t)e * (K / g) * N;
+  const int nout = act ? N / 2 : N;
+  const int n0 = act ? blockIdx.x * SK_COLS : blockIdx.x * NT * SK_COLS;
+  const int coloff = act ? N / 2 : SK_COLS;
+  const int nsteps = (K / 8 + 3) / 4;
+  const int nrounds = (nsteps + MOE_NW * MOE_SPW - 1) / (MOE_NW * MOE_SPW);
+
+  for (int mb = r0; mb < r1; mb += MT * 16) {
+    const int mrows = min(MT * 16, r1 - mb);
+    f32x4 acc[MT][NT][4];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[mt][t][j] = f32x4{0, 0, 0, 0};
+    const f16* A = gather ? X : X + (size_t)mb * K;
+    skinny_wave<false, MT, NT, MOE_SPW>(A, K, gather ? sorted_idx + mb : nullptr, topk, mrows, B,
+                                        S, nullptr, N, K, g, n0, coloff, wave * MOE_SPW, nrounds,
+                                        MOE_NW * MOE_SPW, acc);
+    skinny_block_reduce<MT, NT, MOE_NW>(red, acc);
+    if (wave == 0) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const int row = mt * 16 + 4 * q + rr;
+          if (row >= mrows) continue;
+          f16* yrow = Y + (size_t)(mb + row) * nout;
+          if (act) {
+            const int col = n0 + 4 * c;
+            if (col < nout) {
+              f16x4 o;
+#pragma unroll
+              for (int j = 0; j < 4; ++j) {
+                const float gt = acc[mt][0][j][rr], up = acc[mt][1][j][rr];
+                o[j] = (f16)(gt / (1.0f + __expf(-gt)) * up);
+              }
+              *(f16x4*)(yrow + col) = o;
+            }
+          } else {
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+              const int col = n0 + t * SK_COLS + 4 * c;
+              if (col < nout)
+                *(f16x4*)(yrow + col) = f16x4{(f16)acc[mt][t][0][rr], (f16)acc[mt][t][1][rr],
+                                              (f16)acc[mt][t][2][rr], (f16)acc[mt][t][3][rr]};
+            }
+          }
+        }
+    }
+  }
+}
+
+// out[t, :] = sum_j probs[t, j] * Y[inverse[t*k + j], :]; one block per token,
+// 8 columns per thread.
+__global__ void __launch_bounds__(256)
+k_moe_combine(const f16* __restrict__ Y, const float* __restrict__ probs,
+              const int32_t* __restrict__ inverse, int k, int H, f16* __restrict__ out) {
+  const int t = blockIdx.x;
+  for (int h8 = threadIdx.x; h8 < H / 8; h8 += 256) {
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int j = 0; j < k; ++j) {
+      const float p = probs[(size_t)t * k + j];
+      const f16x8 y = *(const f16x8*)(Y + (size_t)inverse[(size_t)t * k + j] * H + 8 * h8);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] += p * (float)y[i];
+    }
+    f16x8 o;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = (f16)acc[i];
+    *(f16x8*)(out + (size_t)t * H + 8 * h8) = o;
+  }
+}
+
+}  // namespace
+
+// ===========================================================================
+// C ABI
+// ===========================================================================
+extern "C" int mm_moe_sort(const int32_t* expert_ids, int T, int k, int E, int32_t* offsets,
+                           int32_t* sorted_idx, int32_t* inverse, void* stream) {
+  MM_CHECK_ARG(T >= 0 && k > 0, "mm_moe_sort: bad T=%d k=%d", T, k);
+  MM_CHECK_ARG(E > 0 && E <= SORT_THREADS, "mm_moe_sort: num_experts=%d must be in [1, %d]", E,
+               SORT_THREADS);
+  const size_t lds = (size_t)(SORT_WAVES + 1) * E * sizeof(int);
+  hipLaunchKernelGGL(k_moe_sort, dim3(1), dim3(SORT_THREADS), lds, (hipStream_t)stream,
+                     expert_ids, T * k, E, offsets, sorted_idx, inverse);
+  MM_CHECK_LAUNCH("mm_moe_sort");
+  return 0;
+}
+
+extern "C" int mm_moe_grouped_gemm(const uint16_t* X, const int32_t* sorted_idx,
+                                   const int32_t* offsets, int gather, int k, int T,
+                                   const uint32_t* B, const uint16_t* S, int E, int K, int N,
+                                   int g, int act, uint16_t* Y, void* stream) {
+  MM_CHECK_ARG(E > 0 && K > 0 && N > 0 && T >= 0 && k > 0, "mm_moe_grouped_gemm: bad shape");
+  MM_CHECK_ARG(K % 8 == 0, "mm_moe_grouped_gemm: K=%d must be divisible by 8", K);
+  MM_CHECK_ARG(g > 0 && g % 8 == 0 && K % g == 0,
+               "mm_moe_grouped_gemm: group_size=%d must be a multiple of 8 dividing K=%d", g, K);
+  MM_CHECK_ARG(act == 0 || act == 1, "mm_moe_grouped_gemm: act=%d must be 0 or 1", act);
+  MM_CHECK_ARG(act ? (N % 8 == 0) : (N % 4 == 0),
+               "mm_moe_grouped_gemm: N=%d must be divisible by %d", N, act ? 8 : 4);
+  if (T == 0) return 0;
+  const int nout = act ? N / 2 : N;
+  const int tiles = act ? mm_cdiv(nout, SK_COLS) : mm_cdiv(N, 2 * SK_COLS);
+  dim3 grid(tiles, 1, E);
+  const int avg_rows = (T * k + E - 1) / E;
+  if (avg_rows <= 16)
+    hipLaunchKernelGGL(k_moe_grouped<1>, grid, dim3(MOE_NW * 64), 0, (hipStream_t)stream,
+                       (const f16*)X, sorted_idx, offsets, gather, k, B, (const f16*)S, K, N, g,
+                       act, (f16*)Y);
+  else
+    hipLaunchKernelGGL(k_moe_grouped<2>, grid, dim3(MOE_NW * 64), 0, (hipStream_t)stream,
+                       (const f16*)X, sorted_idx, offsets, gather, k, B, (const f16*)S, K, N, g,
+                       act, (f16*)Y);
+  MM_CHECK_LAUNCH("mm_moe_grouped_gemm");
+  return 0;
+}
+
+extern "C" int mm_moe_combine(const uint16_t* Y, const float* probs, const int32_t* inverse,
+                              int T, int k, int H, uint16_t* out, void* stream) {
+  MM_CHECK_ARG(T >= 0 && k > 0 && H > 0, "mm_moe_combine: bad shape");
+  MM_CHECK_ARG(H % 8 == 0, "mm_moe_combine: H=%d must be divisible by 8", H);
+  if (T == 0) return 0;
+  hipLaunchKernelGGL(k_moe_combine, dim3(T), dim3(256), 0, (hipStream_t)stream, (const f16*)Y,
+                     probs, inverse, k, H, (f16*)out);
+  MM_CHECK_LAUNCH("mm_moe_combine");
+  return 0;
+}

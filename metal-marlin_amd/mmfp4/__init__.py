@@ -1,0 +1,20 @@
+"""mmfp4 -- MI355X (gfx950) FP4-E2M1 / INT4 dequant-GEMM and MoE grouped-expert
+path with the Python surface of RESMP-DEV/metal-marlin's quantized linear,
+kernels and moe_dispatch modules.  Kernels live in libmmfp4.so (HIP, C ABI)."""
+
+from .kernels import (FP4_PER_UINT, decode_gemv_fp4, dequant_fp4, dequant_fp4_decode_gemv,
+                      dequant_int4, dequantize_mmfp4, marlin_gemm_fp4, marlin_gemm_fp4_tuned,
+                      marlin_gemm_fused_fp4, marlin_gemm_fused_u4, marlin_gemm_int4, mmfp4_gemm,
+                      select_decode_kernel)
+from .moe_dispatch import (MoEDispatcher, MoEDispatchInfo, compute_expert_load,
+                           compute_load_balancing_loss, gather_for_experts,
+                           group_tokens_by_expert, group_tokens_by_expert_full,
+                           moe_expert_gemm_fp4, moe_mlp_fp4, moe_router_topk,
+                           scatter_expert_outputs)
+from .quantize_fp4 import (E2M1_VALUES, compute_quantization_error, pack_u4_weights,
+                           quantize_fp4, unpack_fp4, unpack_u4_weights)
+from .quantized_linear import (KernelLibrary, MarlinLinear, QuantizedLinear, QuantizedTensor,
+                               dequant_fp4_bulk, dequant_int4_bulk, get_default_library,
+                               quantized_linear)
+
+__version__ = "0.1.0"

@@ -1,0 +1,191 @@
+"""Drop-in FP4 / INT4 dequant-GEMM entry points (the reference's
+`metal_marlin.kernels` GEMM surface), backed by libmmfp4.so on gfx950.
+
+Same names, argument meaning and errors as metal_marlin/kernels_core.py;
+outputs are fp16 like the reference.  Calls are asynchronous on the current
+torch stream (the reference blocks on `waitUntilCompleted`); there is no CPU
+fallback: host tensors raise.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+__all__ = [
+    "marlin_gemm_fp4", "marlin_gemm_fp4_tuned", "marlin_gemm_fused_fp4",
+    "marlin_gemm_int4", "marlin_gemm_fused_u4", "dequant_fp4", "dequant_int4",
+    "dequant_fp4_decode_gemv", "decode_gemv_fp4", "mmfp4_gemm", "dequantize_mmfp4",
+    "select_decode_kernel", "FP4_PER_UINT",
+]
+
+FP4_PER_UINT = 8
+
+
+def _packed(t: torch.Tensor) -> torch.Tensor:
+    if t.dtype not in (torch.int32, torch.uint32):
+        raise TypeError(f"packed weights must be int32/uint32 words, got {t.dtype}")
+    return t.contiguous()
+
+
+def _half(t: torch.Tensor) -> torch.Tensor:
+    return (t if t.dtype == torch.float16 else t.to(torch.float16)).contiguous()
+
+
+def _check_groups(name: str, scales: torch.Tensor, K: int, N: int, group_size: int) -> None:
+    if group_size <= 0 or K % group_size != 0:
+        raise ValueError(f"{name}: K={K} must be divisible by group_size={group_size}")
+    if tuple(scales.shape) != (K // group_size, N):
+        raise ValueError(f"{name}: {name} shape {tuple(scales.shape)} != "
+                         f"({K // group_size}, {N}) for K={K}, group_size={group_size}")
+
+
+def _gemm(kind: str, A: torch.Tensor, B_packed: torch.Tensor, scales: torch.Tensor,
+          zeros: torch.Tensor | None, group_size: int) -> torch.Tensor:
+    dev = _lib.require_device(A, B_packed, scales, zeros)
+    orig_shape = A.shape
+    K = orig_shape[-1]
+    M = 1
+    for d in orig_shape[:-1]:
+        M *= d
+    K_packed, N = B_packed.shape
+    if K_packed * FP4_PER_UINT != K:
+        raise ValueError(f"Packed K {K_packed * FP4_PER_UINT} does not match activations K {K}")
+    _check_groups("scales", scales, K, N, group_size)
+    if zeros is not None:
+        _check_groups("zeros", zeros, K, N, group_size)
+    a = _half(A.reshape(M, K))
+    b = _packed(B_packed)
+    s = _half(scales)
+    out = torch.empty((M, N), dtype=torch.float16, device=dev)
+    ws_bytes = int(_lib.load().mm_gemm_workspace_bytes(M, N, K))
+    ws = _lib.workspace(dev, ws_bytes)
+    st = _lib.stream_of(a)
+    if kind == "fp4":
+        _lib.call("mm_fp4_gemm", _lib.ptr(a), _lib.ptr(b), _lib.ptr(s), _lib.ptr(out), M, N, K,
+                  group_size, _lib.ptr(ws), ws.numel(), st)
+    else:
+        z = _half(zeros)
+        _lib.call("mm_u4_gemm", _lib.ptr(a), _lib.ptr(b), _lib.ptr(s), _lib.ptr(z),
+                  _lib.ptr(out), M, N, K, group_size, _lib.ptr(ws), ws.numel(), st)
+    return out.reshape(*orig_shape[:-1], N)
+
+
+def marlin_gemm_fp4(A: torch.Tensor, B_packed: torch.Tensor, scales: torch.Tensor,
+                    group_size: int = 32) -> torch.Tensor:
+    """C = A @ dequant(B_packed, scales) -- kernels_core.py:1830-1937.
+
+    A [*, K] (any float dtype, computed as fp16), B_packed [K/8, N] int32/uint32
+    Marlin layout, scales [K/group_size, N].  Returns fp16 [*, N].  M <= 32 runs
+    the decode kernel, larger M the MFMA prefill kernel (metal_dispatch.py:
+    4083-4098 chooses by M the same way).
+    """
+    return _gemm("fp4", A, B_packed, scales, None, group_size)
+
+
+def marlin_gemm_fp4_tuned(A, B_packed, scales, group_size: int = 32):
+    """Alias of marlin_gemm_fp4 (kernels_core.py:1939-1947)."""
+    return marlin_gemm_fp4(A, B_packed, scales, group_size)
+
+
+def marlin_gemm_fused_fp4(A, B_packed, scales, group_size: int = 32):
+    """Alias of marlin_gemm_fp4 (kernels_core.py:1949-1957)."""
+    return marlin_gemm_fp4(A, B_packed, scales, group_size)
+
+
+def marlin_gemm_int4(A: torch.Tensor, B_packed: torch.Tensor, scales: torch.Tensor,
+                     zeros: torch.Tensor, group_size: int = 32) -> torch.Tensor:
+    """C = A @ ((q - zeros) * scales) -- kernels_core.py:1959-2066."""
+    return _gemm("u4", A, B_packed, scales, zeros, group_size)
+
+
+def marlin_gemm_fused_u4(A, B_packed, scales, zeros, group_size: int = 32):
+    """Alias of marlin_gemm_int4 (kernels_core.py:2068-2077)."""
+    return marlin_gemm_int4(A, B_packed, scales, zeros, group_size)
+
+
+def dequant_fp4(B_packed: torch.Tensor, scales: torch.Tensor, K: int, N: int,
+                group_size: int = 32) -> torch.Tensor:
+    """[K/8, N] -> [K, N] fp16, bit-exact with the reference dequantizer
+    (kernels_core.py:2079-2133)."""
+    dev = _lib.require_device(B_packed, scales)
+    if tuple(B_packed.shape) != (K // 8, N) or K % 8 != 0:
+        raise ValueError(f"B_packed shape {tuple(B_packed.shape)} != ({K // 8}, {N})")
+    _check_groups("scales", scales, K, N, group_size)
+    b, s = _packed(B_packed), _half(scales)
+    out = torch.empty((K, N), dtype=torch.float16, device=dev)
+    _lib.call("mm_fp4_dequant", _lib.ptr(b), _lib.ptr(s), _lib.ptr(out), K, N, group_size,
+              _lib.stream_of(out))
+    return out
+
+
+def dequant_int4(B_packed: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor, K: int,
+                 N: int, group_size: int = 32) -> torch.Tensor:
+    """INT4 bulk dequant [K/8, N] -> [K, N] fp16 (metal_marlin.py:615-678)."""
+    dev = _lib.require_device(B_packed, scales, zeros)
+    if tuple(B_packed.shape) != (K // 8, N) or K % 8 != 0:
+        raise ValueError(f"B_packed shape {tuple(B_packed.shape)} != ({K // 8}, {N})")
+    _check_groups("scales", scales, K, N, group_size)
+    _check_groups("zeros", zeros, K, N, group_size)
+    b, s, z = _packed(B_packed), _half(scales), _half(zeros)
+    out = torch.empty((K, N), dtype=torch.float16, device=dev)
+    _lib.call("mm_u4_dequant", _lib.ptr(b), _lib.ptr(s), _lib.ptr(z), _lib.ptr(out), K, N,
+              group_size, _lib.stream_of(out))
+    return out
+
+
+def dequant_fp4_decode_gemv(A: torch.Tensor, B_packed: torch.Tensor, scales: torch.Tensor,
+                            K: int, N: int, group_size: int = 128) -> torch.Tensor:
+    """M=1 GEMV, A [K] -> [N] fp16 (kernels_core.py:2135-2200)."""
+    if A.numel() != K:
+        raise ValueError(f"A has {A.numel()} elements, expected K={K}")
+    if B_packed.shape[1] != N:
+        raise ValueError(f"B_packed has N={B_packed.shape[1]}, expected {N}")
+    return marlin_gemm_fp4(A.reshape(1, K), B_packed, scales, group_size).reshape(N)
+
+
+def decode_gemv_fp4(A: torch.Tensor, B_packed: torch.Tensor, B_scales: torch.Tensor,
+                    group_size: int = 128) -> torch.Tensor:
+    """Decode GEMV (kernels_core.py:3755-3831 / :4814): A [K] -> [N] or A [M, K]
+    -> [M, N]; M > 1 is the same fused GEMM."""
+    squeeze = A.ndim == 1
+    A2 = A.reshape(1, -1) if squeeze else A
+    K_packed = B_packed.shape[0]
+    if A2.shape[-1] != K_packed * FP4_PER_UINT:
+        raise ValueError(f"K mismatch: A has K={A2.shape[-1]}, B_packed implies "
+                         f"K={K_packed * FP4_PER_UINT}")
+    out = marlin_gemm_fp4(A2, B_packed, B_scales, group_size)
+    return out.reshape(-1) if squeeze else out
+
+
+def _scales_from_mmfp4(B_scales: torch.Tensor, K: int, N: int, group_size: int) -> torch.Tensor:
+    # The MMFP4 kernels take scales as [N, K/group_size]
+    # (metal_marlin/shaders/mmfp4_gemm.metal:150-151).
+    if tuple(B_scales.shape) != (N, K // group_size):
+        raise ValueError(f"B_scales shape {tuple(B_scales.shape)} != ({N}, {K // group_size})")
+    return B_scales.t().contiguous()
+
+
+def mmfp4_gemm(A: torch.Tensor, B_packed: torch.Tensor, B_scales: torch.Tensor,
+               group_size: int = 128) -> torch.Tensor:
+    """MMFP4 fused GEMM (kernels_core.py:4804-4812 -> MetalKernels.mmfp4_gemm
+    :4550-4633): B_packed [K/8, N], B_scales [N, K/group_size]; A [M, K]."""
+    K = B_packed.shape[0] * FP4_PER_UINT
+    N = B_packed.shape[1]
+    return marlin_gemm_fp4(A, B_packed, _scales_from_mmfp4(B_scales, K, N, group_size),
+                           group_size)
+
+
+def dequantize_mmfp4(packed: torch.Tensor, scales: torch.Tensor,
+                     group_size: int = 128) -> torch.Tensor:
+    """MMFP4 bulk dequant (kernels_core.py:4795-4802) -> [K, N] fp16."""
+    K = packed.shape[0] * FP4_PER_UINT
+    N = packed.shape[1]
+    return dequant_fp4(packed, _scales_from_mmfp4(scales, K, N, group_size), K, N, group_size)
+
+
+def select_decode_kernel(M: int, N: int, K: int) -> str:
+    """Kernel family the library runs for an M x K x N problem (the
+    reference's selector is kernels_core.py:3833-3852)."""
+    return "decode_gemv_fp4" if M <= 32 else "marlin_gemm_fp4"

@@ -1,0 +1,213 @@
+"""MoE token grouping, gather, grouped FP4 expert GEMM and weighted combine
+(the reference's `metal_marlin.moe_dispatch` and `kernels.moe_expert_gemm_fp4`
+surface), on the GPU through libmmfp4.so.
+
+The whole routed-expert pass is one stream of four launches with no host
+synchronisation: stable device counting sort -> grouped gate_up GEMM (token
+gather + SwiGLU fused) -> grouped down GEMM -> deterministic combine.
+"""
+
+from __future__ import annotations
+
+from collections.abc import Sequence
+from dataclasses import dataclass
+
+import torch
+import torch.nn as nn
+
+from . import _lib
+
+
+@dataclass
+class MoEDispatchInfo:
+    """Indexing tensors of a grouped MoE pass (moe_dispatch.py:453-490)."""
+
+    sorted_token_indices: torch.Tensor  # [T*k] token of each sorted assignment
+    sorted_expert_indices: torch.Tensor  # [T*k] slot (0..k-1) of each sorted assignment
+    expert_offsets: torch.Tensor  # [E+1]
+    inverse_indices: torch.Tensor  # [T*k]
+    num_tokens: int
+    top_k: int
+    num_experts: int
+    sorted_indices: torch.Tensor | None = None  # [T*k] int32 flat index t*k+slot
+
+    @property
+    def total_assignments(self) -> int:
+        return self.num_tokens * self.top_k
+
+
+def _sort(expert_ids: torch.Tensor, num_experts: int):
+    """Device counting sort -> (sorted_idx, offsets, inverse), all int32."""
+    dev = _lib.require_device(expert_ids)
+    if expert_ids.dim() != 2:
+        raise ValueError("expert_ids must be [batch, top_k]")
+    T, k = expert_ids.shape
+    ids = expert_ids.to(torch.int32).contiguous()
+    offsets = torch.empty(num_experts + 1, dtype=torch.int32, device=dev)
+    sorted_idx = torch.empty(T * k, dtype=torch.int32, device=dev)
+    inverse = torch.empty(T * k, dtype=torch.int32, device=dev)
+    _lib.call("mm_moe_sort", _lib.ptr(ids), T, k, num_experts, _lib.ptr(offsets),
+              _lib.ptr(sorted_idx), _lib.ptr(inverse), _lib.stream_of(ids))
+    return sorted_idx, offsets, inverse
+
+
+def group_tokens_by_expert(expert_ids: torch.Tensor, num_experts: int):
+    """Stable counting sort of the flattened assignments by expert
+    (moe_dispatch.py:493-555).  Returns int64 (sorted_indices, expert_offsets
+    [E+1], inverse_indices)."""
+    s, o, inv = _sort(expert_ids, num_experts)
+    return s.to(torch.int64), o.to(torch.int64), inv.to(torch.int64)
+
+
+def group_tokens_by_expert_full(expert_ids: torch.Tensor, num_experts: int,
+                                use_gpu: bool = True) -> MoEDispatchInfo:
+    """moe_dispatch.py:726-786.  `use_gpu` is accepted for signature
+    compatibility; the sort always runs on the device."""
+    T, k = expert_ids.shape
+    s, o, inv = _sort(expert_ids, num_experts)
+    s64 = s.to(torch.int64)
+    return MoEDispatchInfo(
+        sorted_token_indices=s64 // k, sorted_expert_indices=s64 % k,
+        expert_offsets=o.to(torch.int64), inverse_indices=inv.to(torch.int64),
+        num_tokens=T, top_k=k, num_experts=num_experts, sorted_indices=s)
+
+
+def gather_for_experts(activations: torch.Tensor, dispatch_info: MoEDispatchInfo) -> torch.Tensor:
+    """X_sorted = X[sorted_token_indices] (moe_dispatch.py:789-809)."""
+    return activations[dispatch_info.sorted_token_indices]
+
+
+def scatter_expert_outputs(expert_outputs: torch.Tensor, expert_probs: torch.Tensor,
+                           dispatch_info: MoEDispatchInfo) -> torch.Tensor:
+    """out[t] = sum_j p[t, j] * y[(t, j)], summed in fp32 in slot order
+    (moe_dispatch.py:812-925)."""
+    dev = _lib.require_device(expert_outputs, expert_probs)
+    T, k = dispatch_info.num_tokens, dispatch_info.top_k
+    H = expert_outputs.shape[1]
+    y = expert_outputs.to(torch.float16).contiguous()
+    p = expert_probs.to(torch.float32).contiguous()
+    inv = dispatch_info.inverse_indices.to(torch.int32).contiguous()
+    out = torch.empty((T, H), dtype=torch.float16, device=dev)
+    _lib.call("mm_moe_combine", _lib.ptr(y), _lib.ptr(p), _lib.ptr(inv), T, k, H, _lib.ptr(out),
+              _lib.stream_of(y))
+    return out if expert_outputs.dtype == torch.float16 else out.to(expert_outputs.dtype)
+
+
+def compute_expert_load(expert_ids: torch.Tensor, num_experts: int) -> torch.Tensor:
+    """Tokens per expert (moe_dispatch.py:930-948)."""
+    return torch.bincount(expert_ids.reshape(-1).to(torch.int64), minlength=num_experts)
+
+
+def compute_load_balancing_loss(expert_probs_pre_topk: torch.Tensor, expert_ids: torch.Tensor,
+                                num_experts: int) -> torch.Tensor:
+    """Switch-Transformer balance loss E * sum_e f_e P_e (moe_dispatch.py:951-982)."""
+    f = compute_expert_load(expert_ids, num_experts).to(torch.float32) / expert_ids.numel()
+    return num_experts * (f * expert_probs_pre_topk.mean(dim=0)).sum()
+
+
+def moe_router_topk(hidden: torch.Tensor, router_weights: torch.Tensor, top_k: int = 2):
+    """softmax(hidden @ router_weights) -> top-k -> renormalise
+    (kernels/moe.py:729-740).  Returns (ids, probs)."""
+    probs = torch.softmax(torch.matmul(hidden, router_weights).to(torch.float32), dim=-1)
+    topk_probs, topk_ids = torch.topk(probs, k=top_k, dim=-1)
+    return topk_ids, topk_probs / topk_probs.sum(dim=-1, keepdim=True)
+
+
+def _grouped(x, sorted_idx, offsets, gather: bool, k: int, T: int, packed, scales,
+             group_size: int, act: int) -> torch.Tensor:
+    E, KP, N = packed.shape
+    K = KP * 8
+    if tuple(scales.shape) != (E, K // group_size, N):
+        raise ValueError(f"scales shape {tuple(scales.shape)} != ({E}, {K // group_size}, {N})")
+    if x.shape[-1] != K:
+        raise ValueError(f"activations K={x.shape[-1]} != packed K={K}")
+    out = torch.empty((T * k, N // 2 if act else N), dtype=torch.float16, device=x.device)
+    _lib.call("mm_moe_grouped_gemm", _lib.ptr(x), _lib.ptr(sorted_idx), _lib.ptr(offsets),
+              int(gather), k, T, _lib.ptr(packed.contiguous()), _lib.ptr(scales.contiguous()),
+              E, K, N, group_size, act, _lib.ptr(out), _lib.stream_of(x))
+    return out
+
+
+def _half(t: torch.Tensor) -> torch.Tensor:
+    return (t if t.dtype == torch.float16 else t.to(torch.float16)).contiguous()
+
+
+def moe_expert_gemm_fp4(activations: torch.Tensor, expert_weights: torch.Tensor,
+                        scales: torch.Tensor, expert_ids: torch.Tensor,
+                        expert_probs: torch.Tensor, group_size: int = 128) -> torch.Tensor:
+    """out[t] = sum_j p[t, j] * (x[t] @ dequant(W[e(t, j)])) (kernels/moe.py:583-727).
+    activations [T, K]; expert_weights [E, K/8, N]; scales [E, K/g, N];
+    expert_ids / expert_probs [T, k].  Returns [T, N] in activations' dtype."""
+    _lib.require_device(activations, expert_weights, scales, expert_ids, expert_probs)
+    T, k = expert_ids.shape
+    E = expert_weights.shape[0]
+    x = _half(activations)
+    s_idx, offs, inv = _sort(expert_ids, E)
+    y = _grouped(x, s_idx, offs, True, k, T, expert_weights, _half(scales), group_size, 0)
+    info = MoEDispatchInfo(s_idx, s_idx, offs, inv, T, k, E, s_idx)
+    out = scatter_expert_outputs(y, expert_probs, info)
+    return out.to(activations.dtype)
+
+
+def moe_mlp_fp4(hidden: torch.Tensor, gate_up_packed: torch.Tensor, gate_up_scales: torch.Tensor,
+                down_packed: torch.Tensor, down_scales: torch.Tensor, expert_ids: torch.Tensor,
+                expert_probs: torch.Tensor, group_size: int = 128) -> torch.Tensor:
+    """Routed-expert SwiGLU MLP over all experts in four launches:
+        h = x @ W_gu[e];  a = silu(h[:, :I]) * h[:, I:];  y = a @ W_dn[e];
+        out[t] = sum_j p[t, j] * y[(t, j)]
+    (moe_dispatch.py:1241-1431 per expert, combined as :812-925).
+    gate_up_packed [E, H/8, 2I], down_packed [E, I/8, H]; scales alike."""
+    _lib.require_device(hidden, gate_up_packed, gate_up_scales, down_packed, down_scales,
+                        expert_ids, expert_probs)
+    T, k = expert_ids.shape
+    E = gate_up_packed.shape[0]
+    x = _half(hidden.reshape(T, -1))
+    s_idx, offs, inv = _sort(expert_ids, E)
+    a = _grouped(x, s_idx, offs, True, k, T, gate_up_packed, _half(gate_up_scales), group_size, 1)
+    y = _grouped(a, s_idx, offs, False, k, T, down_packed, _half(down_scales), group_size, 0)
+    info = MoEDispatchInfo(s_idx, s_idx, offs, inv, T, k, E, s_idx)
+    return scatter_expert_outputs(y, expert_probs, info).to(hidden.dtype)
+
+
+class MoEDispatcher(nn.Module):
+    """Top-k MoE with optional shared expert (moe_dispatch.py:1025-1108):
+    softmax -> top-k (no renormalisation) -> group -> per-expert callables ->
+    weighted combine.  Expert offsets reach the host with one copy per call
+    (the reference does one .item() sync per expert)."""
+
+    def __init__(self, num_experts: int, num_experts_per_tok: int, experts: Sequence,
+                 shared_expert=None, shared_expert_weight: float = 1.0) -> None:
+        super().__init__()
+        self.num_experts = num_experts
+        self.num_experts_per_tok = num_experts_per_tok
+        self.experts = nn.ModuleList(experts)  # type: ignore[arg-type]
+        self.shared_expert = shared_expert
+        self.shared_expert_weight = shared_expert_weight
+
+    def forward(self, hidden: torch.Tensor, gate_logits: torch.Tensor) -> torch.Tensor:
+        if hidden.dim() == 3:
+            batch, seq, hd = hidden.shape
+            flat = hidden.view(-1, hd)
+        else:
+            flat, batch, seq = hidden, None, None
+        if gate_logits.dim() != 2:
+            raise ValueError("gate_logits must be [tokens, num_experts]")
+        if gate_logits.shape[0] != flat.shape[0]:
+            raise ValueError("gate_logits batch must match hidden tokens")
+        probs = gate_logits.softmax(dim=-1)
+        topk_w, topk_i = torch.topk(probs, k=self.num_experts_per_tok, dim=-1)
+        info = group_tokens_by_expert_full(topk_i, self.num_experts)
+        xin = gather_for_experts(flat, info)
+        out_dim = getattr(self.experts[0], "out_features", flat.shape[-1])
+        y = flat.new_empty((xin.shape[0], out_dim))
+        offs = info.expert_offsets.cpu().tolist()
+        for e in range(self.num_experts):
+            a, b = offs[e], offs[e + 1]
+            if a != b:
+                y[a:b] = self.experts[e](xin[a:b])
+        combined = scatter_expert_outputs(y, topk_w, info)
+        if self.shared_expert is not None:
+            combined = combined + self.shared_expert_weight * self.shared_expert(flat)
+        if batch is not None:
+            return combined.view(batch, seq, -1)
+        return combined

@@ -1,0 +1,33 @@
+"""CPU oracle for the FP4 (E2M1) / INT4 dequant-GEMM path and its MoE variant.
+
+TEST INFRASTRUCTURE ONLY.  Nothing in the shipped package (`metal-marlin_amd/`)
+imports this directory.  It is used by `tests/`, by `__graft_entry__.smoke()`
+as the checker, and by `bench.py`'s `cpu_baseline` leg, which times the
+reference's own CPU path (torch dequant + fp32 matmul).
+
+Every function restates, in numpy (or torch-CPU for the timed baseline), an
+algorithm of RESMP-DEV/metal-marlin and cites the reference file:line it follows.
+
+Pinning status (what checks each function against something other than itself):
+
+* `e2m1_decode`, `dequant_fp4`   -- pinned: FP4_E2M1_BITS table and scale
+  known-answers of tests/test_dequant.py, plus an exhaustive closed-form check
+  (16 codes x every finite fp16 scale, float64 product, one rounding).
+* `dequant_u4`                   -- pinned: magic-bias identity and
+  ref_dequant_u4_bulk known answers of tests/test_dequant.py, plus an
+  exhaustive q x integral z x sampled s closed-form check.
+* `quantize_fp4`                 -- pinned: golden vectors written by importing
+  the reference's quantize_fp4.py (tests/golden/make_quantize_fp4_vectors.py),
+  plus the nearest-value invariant on random and crafted midpoint inputs.
+* `pack_u4_weights`              -- partially pinned: round-trip bound
+  |w - (q-z)s| <= s/2 inside the clip range, exact min/max mapping, and the
+  reference test-file quantizer on zero-clip-free inputs.  The reference
+  function itself requires Apple MPS and cannot be imported here, so its
+  half-to-even tie behaviour on exact .5 inputs is "parity unpinned".
+* `gemm_fp4_ref`, `gemm_u4_ref`  -- fp32 dequant+matmul; pinned by the
+  zero / linearity / all-ones-large-K closed forms of tests/test_gemm.py and a
+  brute-force float64 triple loop on tiny shapes.
+* MoE (`group_tokens_by_expert`, `gather`, `combine`, `moe_mlp_ref`) --
+  pinned by the known-answer cases of tests/test_moe.py and a brute-force
+  per-token loop on tiny inputs.
+"""

@@ -1,0 +1,80 @@
+"""The C-ABI library loads, exports exactly what include/mmfp4.h declares, and
+rejects bad arguments before touching the GPU (runs without a GPU)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from mmfp4 import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "mmfp4.h"
+
+
+def declared() -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(mm_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_all_bound_symbols():
+    assert declared() == sorted(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in declared():
+        assert hasattr(lib, name), name
+
+
+@pytest.mark.parametrize("M,N,K,g,msg", [
+    (1, 64, 7, 8, "divisible by 8"),
+    (1, 66, 64, 32, "divisible by 4"),
+    (1, 64, 64, 12, "group_size"),
+    (1, 64, 96, 64, "group_size"),
+])
+def test_gemm_rejects_bad_shapes(M, N, K, g, msg):
+    with pytest.raises(ValueError, match=msg):
+        _lib.call("mm_fp4_gemm", None, None, None, None, M, N, K, g, None, 0, None)
+    with pytest.raises(ValueError, match=msg):
+        _lib.call("mm_u4_gemm", None, None, None, None, None, M, N, K, g, None, 0, None)
+
+
+def test_misaligned_operands_rejected():
+    with pytest.raises(ValueError, match="aligned"):
+        _lib.call("mm_fp4_gemm", ctypes.c_void_p(2), ctypes.c_void_p(16), ctypes.c_void_p(16),
+                  ctypes.c_void_p(16), 1, 64, 64, 32, None, 0, None)
+
+
+def test_other_entry_points_validate():
+    with pytest.raises(ValueError, match="num_experts"):
+        _lib.call("mm_moe_sort", None, 4, 2, 2000, None, None, None, None)
+    with pytest.raises(ValueError, match="act"):
+        _lib.call("mm_moe_grouped_gemm", None, None, None, 1, 2, 4, None, None, 4, 64, 64, 32, 7,
+                  None, None)
+    with pytest.raises(ValueError, match="H="):
+        _lib.call("mm_moe_combine", None, None, None, 4, 2, 12, None, None)
+    with pytest.raises(ValueError, match="group_size"):
+        _lib.call("mm_fp4_dequant", None, None, None, 64, 16, 24, None)
+    with pytest.raises(ValueError, match="divisible by 8"):
+        _lib.call("mm_u4_quantize", None, 16, 12, 4, None, None, None, None)
+
+
+def test_workspace_size_is_sane():
+    lib = _lib.load()
+    assert lib.mm_gemm_workspace_bytes(1, 4096, 14336) >= 4 * 4096
+    assert lib.mm_gemm_workspace_bytes(2048, 14336, 4096) == 65536
+
+
+def test_host_tensors_are_refused():
+    import mmfp4
+    a = torch.zeros(1, 64, dtype=torch.float16)
+    b = torch.zeros(8, 64, dtype=torch.int32)
+    s = torch.zeros(2, 64, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        mmfp4.marlin_gemm_fp4(a, b, s, 32)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        mmfp4.dequant_fp4(b, s, 64, 64, 32)

@@ -1,0 +1,163 @@
+"""GPU parity of the fused FP4 / INT4 dequant-GEMM against the oracle's fp32
+dequant+matmul (max-abs-rel <= 1e-2), plus the
+size-independent properties at the BASELINE shapes."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_helpers import TOL, announce, max_abs_rel, to_dev, to_np
+from oracle import fp4 as ofp4
+
+pytestmark = pytest.mark.gpu
+
+
+def _fp4_problem(rng, M, K, N, g):
+    w = rng.normal(0, 0.02, (N, K)).astype(np.float16)
+    packed, scales = ofp4.quantize_fp4(w, g)
+    a = rng.normal(0, 1, (M, K)).astype(np.float16)
+    return a, packed, scales
+
+
+SMALL = [(1, 128, 128, 32), (2, 256, 192, 64), (5, 512, 256, 128), (16, 1024, 512, 128),
+         (17, 256, 128, 32), (31, 1024, 1000, 8), (32, 4096, 256, 128), (33, 512, 384, 64),
+         (64, 1024, 512, 128), (100, 768, 1024, 128), (128, 256, 256, 32),
+         (129, 512, 260, 64), (256, 2048, 512, 128), (300, 384, 520, 128)]
+
+
+@pytest.mark.parametrize("M,K,N,g", SMALL)
+def test_fp4_gemm_vs_oracle(rng, M, K, N, g):
+    import mmfp4
+    a, packed, scales = _fp4_problem(rng, M, K, N, g)
+    ref = ofp4.gemm_fp4_ref(a, packed, scales, g)
+    announce(f"fp4 gemm M={M} K={K} N={N} g={g}")
+    out = to_np(mmfp4.marlin_gemm_fp4(to_dev(a), to_dev(packed), to_dev(scales), g))
+    assert out.shape == (M, N)
+    assert max_abs_rel(out, ref) <= TOL
+
+
+@pytest.mark.parametrize("M,K,N,g", [(1, 256, 128, 128), (16, 1024, 256, 128),
+                                     (24, 512, 512, 64), (77, 512, 256, 128),
+                                     (256, 1024, 512, 32)])
+def test_u4_gemm_vs_oracle(rng, M, K, N, g):
+    import mmfp4
+    w = rng.normal(0, 0.02, (N, K)).astype(np.float16)
+    packed, s, z = ofp4.pack_u4_weights(w, g)
+    a = rng.normal(0, 1, (M, K)).astype(np.float16)
+    ref = ofp4.gemm_u4_ref(a, packed, s, z, g)
+    announce(f"u4 gemm M={M} K={K} N={N} g={g}")
+    out = to_np(mmfp4.marlin_gemm_int4(to_dev(a), to_dev(packed), to_dev(s), to_dev(z), g))
+    assert max_abs_rel(out, ref) <= TOL
+
+
+def test_fp4_gemm_config1_vs_oracle(rng):
+    """M=1, K=N=4096, g=128, against the CPU oracle."""
+    import mmfp4
+    a, packed, scales = _fp4_problem(rng, 1, 4096, 4096, 128)
+    ref = ofp4.gemm_fp4_ref(a, packed, scales, 128)
+    announce("fp4 gemm config1 M=1 4096x4096")
+    out = to_np(mmfp4.marlin_gemm_fp4(to_dev(a), to_dev(packed), to_dev(scales), 128))
+    assert max_abs_rel(out, ref) <= TOL
+
+
+def _gpu_problem(M, K, N, g, seed=0):
+    """Full-size problem built on the device by the (separately pinned) GPU
+    quantizer; returns a, packed, scales and the unfused fp32 reference
+    dequant(B) (bit-exact kernel) @ A in fp32."""
+    import mmfp4
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    w = (torch.randn((N, K), generator=gen, device="cuda") * 0.02).half()
+    a = torch.randn((M, K), generator=gen, device="cuda").half()
+    packed, scales = mmfp4.quantize_fp4(w, group_size=g)
+    wd = mmfp4.dequant_fp4(packed, scales, K, N, g).float()
+    ref = a.float() @ wd
+    return a, packed, scales, ref
+
+
+LAYERS = [(4096, 6144), (4096, 4096), (4096, 28672), (14336, 4096)]
+
+
+@pytest.mark.parametrize("M", [1, 8, 32])
+@pytest.mark.parametrize("K,N", LAYERS)
+def test_fp4_decode_llama_layers(M, K, N):
+    import mmfp4
+    a, packed, scales, ref = _gpu_problem(M, K, N, 128)
+    announce(f"fp4 decode M={M} K={K} N={N}")
+    out = mmfp4.marlin_gemm_fp4(a, packed, scales, 128)
+    assert max_abs_rel(to_np(out), to_np(ref)) <= TOL
+
+
+@pytest.mark.parametrize("M", [512, 2048])
+@pytest.mark.parametrize("K,N", [(4096, 14336), (14336, 4096)])
+def test_fp4_prefill_config4(M, K, N):
+    import mmfp4
+    a, packed, scales, ref = _gpu_problem(M, K, N, 128)
+    announce(f"fp4 prefill M={M} K={K} N={N}")
+    out = mmfp4.marlin_gemm_fp4(a, packed, scales, 128)
+    assert max_abs_rel(to_np(out), to_np(ref)) <= TOL
+
+
+@pytest.mark.parametrize("M", [1, 16])
+@pytest.mark.parametrize("K,N", LAYERS)
+def test_u4_llama_layers(M, K, N):
+    import mmfp4
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    w = (torch.randn((N, K), generator=gen, device="cuda") * 0.02).half()
+    a = torch.randn((M, K), generator=gen, device="cuda").half()
+    packed, s, z = mmfp4.pack_u4_weights(w, group_size=128)
+    ref = a.float() @ mmfp4.dequant_int4(packed, s, z, K, N, 128).float()
+    announce(f"u4 layer M={M} K={K} N={N}")
+    out = mmfp4.marlin_gemm_int4(a, packed, s, z, 128)
+    assert max_abs_rel(to_np(out), to_np(ref)) <= TOL
+
+
+@pytest.mark.parametrize("M", [1, 20, 64])
+def test_zero_input_and_determinism(M):
+    import mmfp4
+    a, packed, scales, _ = _gpu_problem(M, 14336, 4096, 128, seed=5)
+    announce(f"zero/determinism M={M}")
+    z = mmfp4.marlin_gemm_fp4(torch.zeros_like(a), packed, scales, 128)
+    assert torch.count_nonzero(z).item() == 0
+    o1 = mmfp4.marlin_gemm_fp4(a, packed, scales, 128)
+    o2 = mmfp4.marlin_gemm_fp4(a, packed, scales, 128)
+    assert torch.equal(o1.view(torch.int16), o2.view(torch.int16))
+
+
+@pytest.mark.parametrize("M", [1, 48])
+def test_linearity(M):
+    import mmfp4
+    a, packed, scales, _ = _gpu_problem(M, 4096, 1024, 128, seed=6)
+    b = torch.randn_like(a.float()).half()
+    announce(f"linearity M={M}")
+    lhs = mmfp4.marlin_gemm_fp4((a.float() + b.float()).half(), packed, scales, 128).float()
+    rhs = (mmfp4.marlin_gemm_fp4(a, packed, scales, 128).float()
+           + mmfp4.marlin_gemm_fp4(b, packed, scales, 128).float())
+    assert max_abs_rel(to_np(lhs), to_np(rhs)) <= TOL
+
+
+@pytest.mark.parametrize("M", [1, 32, 100])
+def test_large_k_all_ones(M):
+    """tests/test_gemm.py:531-556: K = 32768 ones against weights 1.0 * 0.5."""
+    import mmfp4
+    K, N = 32768, 256
+    packed = torch.full((K // 8, N), 0x22222222, dtype=torch.int32, device="cuda")
+    scales = torch.full((K // 128, N), 0.5, dtype=torch.float16, device="cuda")
+    announce(f"all-ones K=32768 M={M}")
+    out = mmfp4.marlin_gemm_fp4(torch.ones((M, K), dtype=torch.float16, device="cuda"), packed,
+                                scales, 128)
+    assert torch.all(out == 16384.0).item()
+
+
+def test_split_k_workspace_reuse_across_shapes():
+    """Counters left at zero: interleaved shapes reproduce their first result."""
+    import mmfp4
+    probs = [_gpu_problem(M, K, N, 128, seed=M + K) for M, K, N in
+             [(1, 14336, 4096), (8, 4096, 6144), (32, 14336, 512), (3, 4096, 128)]]
+    announce("workspace reuse")
+    first = [mmfp4.marlin_gemm_fp4(a, p, s, 128) for a, p, s, _ in probs]
+    for _ in range(3):
+        for (a, p, s, _), f in zip(probs, first):
+            assert torch.equal(mmfp4.marlin_gemm_fp4(a, p, s, 128).view(torch.int16),
+                               f.view(torch.int16))
