@@ -55,29 +55,47 @@ def make_weights(torch, mmfp4, K: int, N: int, seed: int, int4: bool = False):
 
 def gpu_sleep_ahead(torch, ms: float = 60.0) -> None:
     """Queue a GPU-side wait so the host can enqueue the timed launches ahead."""
-    torch.cuda._sleep(int(ms * 1e-3 * 2.1e9))
+    torch.cuda._sleep(int(ms * 1e-3 * 1.9e9))   # ~1.9e6 sleep cycles per ms
 
 
-def timed_launches(torch, launches, steps: int, warmup: int):
-    """Run `launches` (list of per-step lists of callables) warmup + steps
-    times; returns (total_ms over `steps`, per-launch ms list)."""
-    nper = len(launches[0])
+def timed_launches(torch, launches, steps: int, warmup: int) -> float:
+    """Run `launches` (list of per-step lists of callables, rotated) for
+    `warmup` untimed then `steps` timed steps; returns ms over the timed steps
+    (HIP events on the launch stream; only two events, so nothing is inserted
+    between the kernels).  The launches are queued behind a GPU sleep sized
+    from the measured host enqueue rate; if the sleep ran out before the host
+    finished enqueueing (the GPU could have idled), the run is repeated with a
+    longer sleep."""
+    t_host = time.perf_counter()
     for s in range(warmup):
         for fn in launches[s % len(launches)]:
             fn()
+    per_launch_s = (time.perf_counter() - t_host) / max(1, warmup * len(launches[0]))
     torch.cuda.synchronize()
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps * nper + 1)]
-    gpu_sleep_ahead(torch, 20.0 + 0.05 * steps * nper)
-    ev[0].record()
-    i = 1
-    for s in range(steps):
-        for fn in launches[s % len(launches)]:
-            fn()
-            ev[i].record()
-            i += 1
-    torch.cuda.synchronize()
-    per = [ev[j].elapsed_time(ev[j + 1]) for j in range(len(ev) - 1)]
-    return ev[0].elapsed_time(ev[-1]), per
+    sleep_ms = 2.0 + 3e3 * per_launch_s * steps * len(launches[0])
+    for _ in range(6):
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        gpu_sleep_ahead(torch, sleep_ms)
+        t0.record()
+        for s in range(steps):
+            for fn in launches[s % len(launches)]:
+                fn()
+        starved = t0.query()          # sleep already over while still enqueueing
+        t1.record()
+        torch.cuda.synchronize()
+        if not starved:
+            return t0.elapsed_time(t1)
+        sleep_ms *= 3
+    raise RuntimeError("could not queue the timed launches ahead of the GPU")
+
+
+def per_shape_us(torch, launches, reps: int = 40) -> list[float]:
+    """Average µs per launch of each step position, timed in its own batch."""
+    out = []
+    for i in range(len(launches[0])):
+        seq = [[step[i]] for step in launches]
+        out.append(1e3 * timed_launches(torch, seq, reps, 2) / reps)
+    return out
 
 
 def run_layer_bench(torch, mmfp4, M: int, steps: int, warmup: int, int4: bool = False):
@@ -100,17 +118,15 @@ def run_layer_bench(torch, mmfp4, M: int, steps: int, warmup: int, int4: bool = 
             else:
                 step.append(lambda a=a, w=wt: mmfp4.marlin_gemm_fp4(a, w[0], w[1], G))
         launches.append(step)
-    total_ms, per = timed_launches(torch, launches, steps, warmup)
+    total_ms = timed_launches(torch, launches, steps, warmup)
     step_bytes = sum(alg_bytes(M, K, N, int4) for _, K, N in LLAMA_LAYER)
     per_shape = {}
-    for idx, (name, K, N) in enumerate(LLAMA_LAYER):
-        ts = per[idx::len(LLAMA_LAYER)]
-        us = 1e3 * sum(ts) / len(ts)
+    for (name, K, N), us in zip(LLAMA_LAYER, per_shape_us(torch, launches)):
         per_shape[name] = {"K": K, "N": N, "us": round(us, 3),
                            "GBps": round(alg_bytes(M, K, N, int4) / (us * 1e3), 1)}
     return {"ms_per_step": total_ms / steps, "step_bytes": step_bytes,
-            "launch_us_avg": 1e3 * sum(per) / len(per), "per_shape": per_shape,
-            "copies": copies}
+            "launch_us_avg": 1e3 * total_ms / (steps * len(LLAMA_LAYER)),
+            "per_shape": per_shape, "copies": copies}
 
 
 def run_prefill_bench(torch, mmfp4, M: int, steps: int, warmup: int):
@@ -119,16 +135,27 @@ def run_prefill_bench(torch, mmfp4, M: int, steps: int, warmup: int):
     acts = {K: torch.randn((M, K), generator=gen, device="cuda").half() for _, K, _ in PREFILL}
     step = [lambda a=acts[K], w=w: mmfp4.marlin_gemm_fp4(a, w[0], w[1], G)
             for (_, K, _), w in zip(PREFILL, ws)]
-    total_ms, per = timed_launches(torch, [step], steps, warmup)
+    total_ms = timed_launches(torch, [step], steps, warmup)
     flops = sum(2 * M * K * N for _, K, N in PREFILL)
     per_shape = {}
-    for idx, (name, K, N) in enumerate(PREFILL):
-        ts = per[idx::len(PREFILL)]
-        us = 1e3 * sum(ts) / len(ts)
+    for (name, K, N), us in zip(PREFILL, per_shape_us(torch, [step], reps=max(3, steps))):
         per_shape[name] = {"K": K, "N": N, "us": round(us, 2),
                            "TFLOPs": round(2 * M * K * N / (us * 1e-6) / 1e12, 1)}
     return {"ms_per_step": total_ms / steps, "flops": flops, "per_shape": per_shape,
-            "launch_us_avg": 1e3 * sum(per) / len(per)}
+            "launch_us_avg": 1e3 * total_ms / (steps * len(PREFILL))}
+
+
+def measured_traffic(name: str) -> float | None:
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary (FETCH_SIZE
+    and WRITE_SIZE runs of `bench.py --pmc-probe`, calibrated on a known copy)."""
+    path = ROOT / "profiles" / name
+    try:
+        for line in path.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return float(line.split(":", 1)[1])
+    except OSError:
+        return None
+    return None
 
 
 def cpu_baseline(budget_s: float = 15.0):
@@ -169,6 +196,35 @@ def cpu_baseline(budget_s: float = 15.0):
                       f"(torch-CPU fp32 dequant+matmul, {platform.processor() or 'host'})"}
 
 
+def pmc_probe(torch, mmfp4) -> int:
+    """Dispatches whose hardware counters calibrate and measure HBM traffic:
+    one copy of 512 MiB (known: 512 MiB read + 512 MiB written), then every
+    Llama-layer GEMM at M=1 on 4 rotated weight copies x 5, then the two
+    M=2048 prefill GEMMs x 2."""
+    src = torch.empty(512 << 20, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    for _, K, N in LLAMA_LAYER:
+        ws = [make_weights(torch, mmfp4, K, N, 300 + c) for c in range(4)]
+        a = torch.randn((1, K), device="cuda").half()
+        for _ in range(5):
+            for w in ws:
+                mmfp4.marlin_gemm_fp4(a, w[0], w[1], G)
+        torch.cuda.synchronize()
+        del ws
+    for _, K, N in PREFILL:
+        w = make_weights(torch, mmfp4, K, N, 400)
+        a = torch.randn((2048, K), device="cuda").half()
+        for _ in range(2):
+            mmfp4.marlin_gemm_fp4(a, w[0], w[1], G)
+        torch.cuda.synchronize()
+    print(json.dumps({"pmc_probe": "done"}))
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -176,6 +232,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--all", action="store_true", help="also report configs 1, 3, 5 and M=8/32")
+    ap.add_argument("--pmc-probe", action="store_true",
+                    help="no timing: run a 512 MiB copy (counter calibration) then the M=1 layer "
+                         "GEMMs and the M=2048 prefill GEMMs, for rocprofv3 --pmc runs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only: the FP4 dequant-GEMM "
@@ -189,6 +248,8 @@ def main() -> int:
         return 1
     import mmfp4
 
+    if args.pmc_probe:
+        return pmc_probe(torch, mmfp4)
     torch.cuda.synchronize()
     layer = run_layer_bench(torch, mmfp4, 1, args.steps, args.warmup)
     pre = run_prefill_bench(torch, mmfp4, 2048, max(5, args.steps // 20), max(2, args.warmup // 10))
@@ -214,7 +275,9 @@ def main() -> int:
                    "weight_copies_rotated": layer["copies"]},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None, "kernel": "k_skinny (M<=32 decode path)",
+                     "traffic": measured_traffic("k_skinny_llama3_layer_m1.md"),
+                     "traffic_source": "profiles/k_skinny_llama3_layer_m1.md",
+                     "kernel": "k_skinny (M<=32 decode path)",
                      "launch_us_avg": round(layer["launch_us_avg"], 3)},
         "per_shape_m1": layer["per_shape"],
         "prefill_m2048": {"tflops": round(tflops, 1), "frac_fp16_peak": round(tflops /

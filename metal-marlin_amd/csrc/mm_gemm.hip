@@ -24,14 +24,16 @@
 namespace {
 using namespace mmsk;
 
+constexpr int SK_RED_BATCH = 8;   // partial-sum loads in flight per thread
+
 // Dense skinny kernel.  grid = (ceil(N / (NT*64)), ksplit).
-template <bool INT4, int MT, int NT, int SPW, int NW>
+template <bool INT4, int MT, int NT, int SPW, int NW, int FL>
 __global__ void __launch_bounds__(NW * 64)
 k_skinny(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
          const f16* __restrict__ S, const f16* __restrict__ Z, f16* __restrict__ C, int ldc,
          int M, int N, int K, int g, int nrounds, float* __restrict__ part,
          uint32_t* __restrict__ counters) {
-  constexpr int RED = (NW / 2 > 0 ? NW / 2 : 1) * MT * NT * 16 * 64;
+  constexpr int RED = (NW > 1 ? NW - 1 : 1) * MT * NT * 16 * 64;
   __shared__ float red[RED];
   __shared__ uint32_t s_last;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -49,7 +51,7 @@ k_skinny(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc[mt][t][j] = f32x4{0, 0, 0, 0};
 
-  skinny_wave<INT4, MT, NT, SPW>(A, lda, nullptr, 1, M, B, S, Z, N, K, g, n0, SK_COLS,
+  skinny_wave<INT4, MT, NT, SPW, FL>(A, lda, nullptr, 1, M, B, S, Z, N, K, g, n0, SK_COLS,
                                  blk_st0 + wave * SPW, nrounds, NW * SPW, acc);
   skinny_block_reduce<MT, NT, NW>(red, acc);
 
@@ -96,7 +98,10 @@ k_skinny(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
         }
       }
   }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  // The partials are agent-scope (write-through) stores: wait until they are
+  // acknowledged before the arrival counter can make them visible to the last
+  // block.  (A workgroup-scope fence alone does not wait for them.)
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0) {
     const uint32_t prev = __hip_atomic_fetch_add(&counters[blockIdx.x], 1u, __ATOMIC_RELAXED,
@@ -105,26 +110,37 @@ k_skinny(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
   }
   __syncthreads();
   if (!s_last) return;
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-  // Every thread of the last block sums a share of the (row, 4-column) items.
+  // One thread per (row, 4-column) item sums the splits in order; the loads of
+  // SK_RED_BATCH splits are issued together so the chain is ksplit/8 trips.
   constexpr int COLS = NT * SK_COLS;
-  const int nitems = MT * 16 * (COLS / 4);
+  const int nitems = min(M, MT * 16) * (COLS / 4);
   for (int e = threadIdx.x; e < nitems; e += NW * 64) {
     const int row = e / (COLS / 4), col = n0 + 4 * (e % (COLS / 4));
-    if (row < M && col < N) {
-      float v[4] = {0, 0, 0, 0};
-      for (int y = 0; y < ksplit; ++y) {
+    if (col >= N) continue;
+    float v[4] = {0, 0, 0, 0};
+    for (int y0 = 0; y0 < ksplit; y0 += SK_RED_BATCH) {
+      float ld[SK_RED_BATCH][4];
+#pragma unroll
+      for (int i = 0; i < SK_RED_BATCH; ++i) {
+        const int y = min(y0 + i, ksplit - 1);
         const float* src = part + ((size_t)y * M + row) * N + col;
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          v[j] += __hip_atomic_load(src + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          ld[i][j] = __hip_atomic_load(src + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
-      *(f16x4*)(C + (size_t)row * ldc + col) = f16x4{(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
+#pragma unroll
+      for (int i = 0; i < SK_RED_BATCH; ++i)
+        if (y0 + i < ksplit)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) v[j] += ld[i][j];
     }
+    *(f16x4*)(C + (size_t)row * ldc + col) = f16x4{(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
   }
   if (threadIdx.x == 0)
     __hip_atomic_store(&counters[blockIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+
+
 
 // ===========================================================================
 // Prefill path
@@ -254,9 +270,26 @@ k_prefill(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
 // ===========================================================================
 // Host-side planning
 // ===========================================================================
-constexpr int SK_NW = 4;
-constexpr int SK_SPW = 4;
-constexpr int SK_NT = 2;
+#ifndef MM_SK_NW
+#define MM_SK_NW 8          // waves per skinny block (power of two)
+#endif
+#ifndef MM_SK_SPW1
+#define MM_SK_SPW1 8        // 32-k steps per wave per round, M <= 16
+#endif
+#ifndef MM_SK_SPW2
+#define MM_SK_SPW2 4        // 32-k steps per wave per round, 16 < M <= 32
+#endif
+#ifndef MM_SK_KS2
+#define MM_SK_KS2 4         // max K split for 16 < M <= 32 (bounds partial traffic)
+#endif
+#ifndef MM_SK_MAXBLOCKS
+#define MM_SK_MAXBLOCKS 2048
+#endif
+constexpr int SK_NW = MM_SK_NW;
+template <int MT> constexpr int sk_spw() { return MT == 1 ? MM_SK_SPW1 : MM_SK_SPW2; }
+// One 64-column virtual-tile quad per block: more column tiles means fewer
+// K splits (less partial-sum traffic) for the same parallelism.
+template <int MT> constexpr int sk_nt() { return 1; }
 
 struct SkinnyPlan {
   int ksplit;
@@ -266,15 +299,18 @@ struct SkinnyPlan {
 
 SkinnyPlan plan_skinny(int M, int N, int K) {
   SkinnyPlan p;
+  const int nt = 1;
+  const int spw = M <= 16 ? sk_spw<1>() : sk_spw<2>();
   const int nsteps = (K / 8 + 3) / 4;                  // 32-k steps
-  const int slab = SK_NW * SK_SPW;                     // steps per block round
+  const int slab = SK_NW * spw;                        // steps per block round
   const int blocks_k = mm_cdiv(nsteps, slab);          // block-rounds along K
-  p.ntiles = mm_cdiv(N, SK_NT * SK_COLS);
-  // Aim for ~1024 blocks; a round is the minimum work of a block.  Larger M
-  // means more partial-sum traffic per split, so split less.
-  const int target = M <= 16 ? 1024 : 512;
-  int ks = mm_cdiv(target, p.ntiles);
-  if (ks > blocks_k) ks = blocks_k;
+  p.ntiles = mm_cdiv(N, nt * SK_COLS);
+  // One round per block (every load of a wave in flight at once) unless that
+  // makes more than ~2048 blocks; for M > 16 cap the split at 8 to bound the
+  // partial-sum traffic (ksplit * M * N * 4 bytes each way).
+  int ks = blocks_k;
+  if ((long)ks * p.ntiles > MM_SK_MAXBLOCKS) ks = mm_cdiv(MM_SK_MAXBLOCKS, p.ntiles);
+  if (M > 16 && ks > MM_SK_KS2) ks = MM_SK_KS2;
   if (ks < 1) ks = 1;
   p.nrounds = mm_cdiv(blocks_k, ks);
   p.ksplit = mm_cdiv(blocks_k, p.nrounds);
@@ -297,8 +333,9 @@ int launch_skinny(const f16* A, int lda, const uint32_t* B, const f16* S, const 
                   int ldc, int M, int N, int K, int g, void* ws, size_t ws_bytes,
                   hipStream_t st) {
   const SkinnyPlan p = plan_skinny(M, N, K);
+  constexpr int NT = sk_nt<MT>();
   MM_CHECK_ARG(p.ntiles <= SK_MAX_TILES, "gemm: N=%d exceeds the supported %d columns", N,
-               SK_MAX_TILES * SK_NT * SK_COLS);
+               SK_MAX_TILES * NT * SK_COLS);
   uint32_t* counters = (uint32_t*)ws;
   float* part = nullptr;
   if (p.ksplit > 1) {
@@ -308,11 +345,24 @@ int launch_skinny(const f16* A, int lda, const uint32_t* B, const f16* S, const 
     part = (float*)((char*)ws + SK_COUNTER_BYTES);
   }
   dim3 grid(p.ntiles, p.ksplit);
-  hipLaunchKernelGGL((k_skinny<INT4, MT, SK_NT, SK_SPW, SK_NW>), grid, dim3(SK_NW * 64), 0, st, A,
-                     lda, B, S, Z, C, ldc, M, N, K, g, p.nrounds, part, counters);
+  constexpr int SPW = sk_spw<MT>();
+  const int fl = flush_steps(g, SPW);
+#define MM_LAUNCH_SK(FLV)                                                                   \
+  hipLaunchKernelGGL((k_skinny<INT4, MT, NT, SPW, SK_NW, FLV>), grid, dim3(SK_NW * 64), 0, st, \
+                     A, lda, B, S, Z, C, ldc, M, N, K, g, p.nrounds, part, counters)
+  switch (fl) {
+    case 1: MM_LAUNCH_SK(1); break;
+    case 2: MM_LAUNCH_SK(2); break;
+    case 4: MM_LAUNCH_SK(4 <= SPW ? 4 : 0); break;
+    case 8: MM_LAUNCH_SK(8 <= SPW ? 8 : 0); break;
+    default: MM_LAUNCH_SK(0); break;
+  }
+#undef MM_LAUNCH_SK
   MM_CHECK_LAUNCH("gemm(skinny)");
   return 0;
 }
+
+
 
 template <bool INT4, int WM, int WN, int RB>
 int launch_prefill(const f16* A, int lda, const uint32_t* B, const f16* S, const f16* Z, f16* C,

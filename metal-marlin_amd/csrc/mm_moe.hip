@@ -102,14 +102,14 @@ k_moe_sort(const int32_t* __restrict__ ids, int n, int E, int32_t* __restrict__ 
 constexpr int MOE_NW = 4;
 constexpr int MOE_SPW = 4;
 
-template <int MT>
+template <int MT, int FL>
 __global__ void __launch_bounds__(MOE_NW * 64)
 k_moe_grouped(const f16* __restrict__ X, const int32_t* __restrict__ sorted_idx,
               const int32_t* __restrict__ offsets, int gather, int topk,
               const uint32_t* __restrict__ Ball, const f16* __restrict__ Sall, int K, int N,
               int g, int act, f16* __restrict__ Y) {
   constexpr int NT = 2;
-  __shared__ float red[(MOE_NW / 2) * MT * NT * 16 * 64];
+  __shared__ float red[(MOE_NW - 1) * MT * NT * 16 * 64];
   const int e = blockIdx.z;
   const int r0 = offsets[e], r1 = offsets[e + 1];
   if (r1 <= r0) return;
@@ -133,7 +133,7 @@ k_moe_grouped(const f16* __restrict__ X, const int32_t* __restrict__ sorted_idx,
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[mt][t][j] = f32x4{0, 0, 0, 0};
     const f16* A = gather ? X : X + (size_t)mb * K;
-    skinny_wave<false, MT, NT, MOE_SPW>(A, K, gather ? sorted_idx + mb : nullptr, topk, mrows, B,
+    skinny_wave<false, MT, NT, MOE_SPW, FL>(A, K, gather ? sorted_idx + mb : nullptr, topk, mrows, B,
                                         S, nullptr, N, K, g, n0, coloff, wave * MOE_SPW, nrounds,
                                         MOE_NW * MOE_SPW, acc);
     skinny_block_reduce<MT, NT, MOE_NW>(red, acc);
@@ -167,6 +167,7 @@ k_moe_grouped(const f16* __restrict__ X, const int32_t* __restrict__ sorted_idx,
           }
         }
     }
+    __syncthreads();   // wave 0 has read `red` before the next chunk overwrites it
   }
 }
 
@@ -224,14 +225,27 @@ extern "C" int mm_moe_grouped_gemm(const uint16_t* X, const int32_t* sorted_idx,
   const int tiles = act ? mm_cdiv(nout, SK_COLS) : mm_cdiv(N, 2 * SK_COLS);
   dim3 grid(tiles, 1, E);
   const int avg_rows = (T * k + E - 1) / E;
-  if (avg_rows <= 16)
-    hipLaunchKernelGGL(k_moe_grouped<1>, grid, dim3(MOE_NW * 64), 0, (hipStream_t)stream,
-                       (const f16*)X, sorted_idx, offsets, gather, k, B, (const f16*)S, K, N, g,
-                       act, (f16*)Y);
-  else
-    hipLaunchKernelGGL(k_moe_grouped<2>, grid, dim3(MOE_NW * 64), 0, (hipStream_t)stream,
-                       (const f16*)X, sorted_idx, offsets, gather, k, B, (const f16*)S, K, N, g,
-                       act, (f16*)Y);
+  const int fl = flush_steps(g, MOE_SPW);
+#define MM_LAUNCH_MOE(MTV, FLV)                                                              \
+  hipLaunchKernelGGL((k_moe_grouped<MTV, FLV>), grid, dim3(MOE_NW * 64), 0, (hipStream_t)stream, \
+                     (const f16*)X, sorted_idx, offsets, gather, k, B, (const f16*)S, K, N, g,  \
+                     act, (f16*)Y)
+  if (avg_rows <= 16) {
+    switch (fl) {
+      case 1: MM_LAUNCH_MOE(1, 1); break;
+      case 2: MM_LAUNCH_MOE(1, 2); break;
+      case 4: MM_LAUNCH_MOE(1, 4); break;
+      default: MM_LAUNCH_MOE(1, 0); break;
+    }
+  } else {
+    switch (fl) {
+      case 1: MM_LAUNCH_MOE(2, 1); break;
+      case 2: MM_LAUNCH_MOE(2, 2); break;
+      case 4: MM_LAUNCH_MOE(2, 4); break;
+      default: MM_LAUNCH_MOE(2, 0); break;
+    }
+  }
+#undef MM_LAUNCH_MOE
   MM_CHECK_LAUNCH("mm_moe_grouped_gemm");
   return 0;
 }

@@ -1,16 +1,29 @@
-// Skinny (decode-shaped) MFMA core shared by the dense and grouped GEMMs.
-// Weights stream HBM -> registers -> MFMA 16x16x32 with no LDS staging; the
-// M rows ride in the 16-row MFMA operand (zero padded).
+// Skinny (decode-shaped, M <= 32) MFMA core shared by the dense and grouped
+// GEMMs.  Weights stream HBM -> registers -> MFMA 16x16x32 with no LDS
+// staging; the M rows ride in the 16-row MFMA operand.
+//
+// Lane l = 16*q + c of a wave, at 32-k step st:
+//   B: one 16-byte load = word row kp = 4*st + q, columns n + 4c .. n + 4c + 3;
+//      word j feeds "virtual" column tile j (its column c is matrix column 4c + j)
+//   A: row 16*mt + c, k = 8*kp .. 8*kp + 7 (the 16x16x32 operand layout)
+//   C: tile (mt, t, j), lane holds rows 16*mt + 4*q + r (r = 0..3), column 4c + j.
+//
+// Group scales: when the group size is a multiple of 32 (FL > 0) a group
+// covers whole steps and the same group for every lane, so the MFMAs of a
+// group accumulate unscaled E2M1 values (or q - z for INT4) and the group
+// sum is multiplied by the fp32 scale once ("post-scale"); the per-word decode
+// is then four packed converts.  Other group sizes (FL == 0) scale every
+// word in fp16 before the MFMA (the reference's rounding of each weight).
 #pragma once
 #include "mm_common.h"
 
 namespace mmsk {
 
-constexpr int SK_COLS = 64;   // columns covered by one 16x16 MFMA "virtual tile" quad
+constexpr int SK_COLS = 64;   // columns of one virtual-tile quad
 
+// Pre-scaled word decode (exact reference fp16 weights).
 template <bool INT4>
 struct WordDq;
-
 template <>
 struct WordDq<false> {
   MM_DEV static f16x8 run(uint32_t w, f16 s, f16 /*nz*/) { return dq_fp4_word(w, f16x2{s, s}); }
@@ -22,105 +35,174 @@ struct WordDq<true> {
   }
 };
 
-// One wave's contribution: `nst` steps of 32 k (4 word rows) starting at
-// step `st0`, stepping by `ststride`, over NT column tiles of 64 columns
-// (tile t starts at column n0 + t*coloff) and MT 16-row groups.
-//   lane = 16*q + c: B word row 4*st + q, columns n + 4c .. n + 4c + 3,
-//   A row 16*mt + c, k = 8*(4*st + q) .. +8 (the MFMA 16x16x32 operand layout).
-template <bool INT4, int MT, int NT, int SPW>
+// Unscaled word decode: E2M1 values, or fp16(q - z) for INT4.
+MM_DEV f16x8 raw_fp4_word(uint32_t w) {
+  const f16x2 p0 = e2m1_pair_c<0>(w), p1 = e2m1_pair_c<1>(w);
+  const f16x2 p2 = e2m1_pair_c<2>(w), p3 = e2m1_pair_c<3>(w);
+  return f16x8{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+}
+MM_DEV f16x8 raw_u4_word(uint32_t w, f16x2 negz2) {
+  const f16x2 m1024 = {(f16)-1024.0f, (f16)-1024.0f};
+  const f16x2 p0 = (u4_pair(w, 0) + m1024) + negz2;
+  const f16x2 p1 = (u4_pair(w, 8) + m1024) + negz2;
+  const f16x2 p2 = (u4_pair(w, 16) + m1024) + negz2;
+  const f16x2 p3 = (u4_pair(w, 24) + m1024) + negz2;
+  return f16x8{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+}
+
+template <typename T>
+MM_DEV const T* at_bytes(const void* base, uint32_t off) {
+  return (const T*)((const char*)base + off);
+}
+
+// One wave's contribution over `nrounds` rounds of SPW consecutive 32-k steps:
+// round r covers steps st0 + r*ststride .. + SPW - 1.  NT column-tile quads
+// start at n0 + t*coloff.  FL: steps per scale flush (> 0, power of two,
+// <= SPW, and group_size == 32*FL*k for an integer k), or 0 for pre-scale.
+// Rows >= M and columns past N compute values that are never stored: their
+// addresses are clamped into the matrix so no load is predicated.
+template <bool INT4, int MT, int NT, int SPW, int FL>
 MM_DEV void skinny_wave(const f16* __restrict__ A, int lda, const int* __restrict__ rowmap,
                         int rowdiv, int M, const uint32_t* __restrict__ B,
                         const f16* __restrict__ S, const f16* __restrict__ Z, int N, int K, int g,
                         int n0, int coloff, int st0, int nrounds, int ststride,
                         f32x4 (&acc)[MT][NT][4]) {
+  static_assert(FL == 0 || (SPW % FL == 0), "flush interval must divide the round");
   const int lane = threadIdx.x & 63;
   const int c = lane & 15, q = lane >> 4;
   const int KP = K >> 3;
+  const int nsteps = (KP + 3) >> 2;
 
-  // A row pointers are fixed for the whole K loop.
-  const f16* arow[MT];
-  bool mok[MT];
+  uint32_t aoff[MT];                       // byte offset of A[row][0]
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
-    const int m = mt * 16 + c;
-    mok[mt] = m < M;
-    int r = m;
-    if (rowmap != nullptr && mok[mt]) r = rowmap[m] / rowdiv;
-    arow[mt] = A + (size_t)(mok[mt] ? r : 0) * lda;
+    const int m = min(mt * 16 + c, M - 1);
+    const int r = rowmap != nullptr ? rowmap[m] / rowdiv : m;
+    aoff[mt] = (uint32_t)r * (uint32_t)lda * 2u;
   }
-  int ncol[NT];
-  bool nok[NT];
+  uint32_t coff[NT];                       // column index of this lane's first column
 #pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    ncol[t] = n0 + t * coloff + 4 * c;
-    nok[t] = ncol[t] < N;
-  }
+  for (int t = 0; t < NT; ++t) coff[t] = (uint32_t)min(n0 + t * coloff + 4 * c, N - 4);
 
   for (int r = 0; r < nrounds; ++r) {
+    const int stb = st0 + r * ststride;    // wave-uniform
+    if (stb >= nsteps) break;
     u32x4 w[SPW][NT];
-    f16x4 s[SPW][NT];
-    f16x4 z[SPW][NT];
     f16x8 a[SPW][MT];
-    // Issue every load of the round before any math.
+    // Issue every weight/activation load of the round before any math.
 #pragma unroll
     for (int i = 0; i < SPW; ++i) {
-      const int st = st0 + r * ststride + i;
-      const int kp = 4 * st + q;
-      const bool kok = kp < KP;
-      const int gi = kok ? (kp * 8) / g : 0;
+      const int kp = min(4 * min(stb + i, nsteps - 1) + q, KP - 1);
 #pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        const bool ok = kok && nok[t];
-        w[i][t] = ok ? *(const u32x4*)(B + (size_t)kp * N + ncol[t]) : u32x4{0, 0, 0, 0};
-        s[i][t] = ok ? *(const f16x4*)(S + (size_t)gi * N + ncol[t]) : f16x4{0, 0, 0, 0};
-        if constexpr (INT4)
-          z[i][t] = ok ? *(const f16x4*)(Z + (size_t)gi * N + ncol[t]) : f16x4{0, 0, 0, 0};
-      }
+      for (int t = 0; t < NT; ++t)
+        w[i][t] = *at_bytes<u32x4>(B, ((uint32_t)kp * (uint32_t)N + coff[t]) * 4u);
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
-        a[i][mt] = (kok && mok[mt]) ? *(const f16x8*)(arow[mt] + (size_t)kp * 8)
-                                    : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+        a[i][mt] = *at_bytes<f16x8>(A, aoff[mt] + (uint32_t)kp * 16u);
     }
+    // Steps past K (a partial last step, or a round overhanging the end)
+    // contribute zero through a zeroed activation operand.
+    if (stb + SPW > nsteps || (K & 31) != 0) {
 #pragma unroll
-    for (int i = 0; i < SPW; ++i) {
+      for (int i = 0; i < SPW; ++i) {
+        const bool valid = stb + i < nsteps && 4 * (stb + i) + q < KP;
 #pragma unroll
-      for (int t = 0; t < NT; ++t) {
+        for (int mt = 0; mt < MT; ++mt)
+          if (!valid) a[i][mt] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+      }
+    }
+
+    if constexpr (FL == 0) {
+      // Pre-scale: each lane's own group, every step.
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          f16 nz = 0;
-          if constexpr (INT4) nz = -clamp_zero(z[i][t][j]);
-          const f16x8 b = WordDq<INT4>::run(w[i][t][j], sanitize_scale(s[i][t][j]), nz);
+      for (int i = 0; i < SPW; ++i) {
+        const int kp = min(4 * min(stb + i, nsteps - 1) + q, KP - 1);
+        const uint32_t gi = (uint32_t)((kp * 8) / g);
 #pragma unroll
-          for (int mt = 0; mt < MT; ++mt)
-            acc[mt][t][j] =
-                __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i][mt], b, acc[mt][t][j], 0, 0, 0);
+        for (int t = 0; t < NT; ++t) {
+          const f16x4 s4 = *at_bytes<f16x4>(S, (gi * (uint32_t)N + coff[t]) * 2u);
+          f16x4 z4 = {0, 0, 0, 0};
+          if constexpr (INT4) z4 = *at_bytes<f16x4>(Z, (gi * (uint32_t)N + coff[t]) * 2u);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            f16 nz = 0;
+            if constexpr (INT4) nz = -clamp_zero(z4[j]);
+            const f16x8 b = WordDq<INT4>::run(w[i][t][j], sanitize_scale(s4[j]), nz);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+              acc[mt][t][j] =
+                  __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i][mt], b, acc[mt][t][j], 0, 0, 0);
+          }
         }
+      }
+    } else {
+      // Post-scale: one group per FL steps, uniform across the wave.
+#pragma unroll
+      for (int f = 0; f < SPW / FL; ++f) {
+        const int stg = min(stb + f * FL, nsteps - 1);
+        const uint32_t gi = (uint32_t)((stg * 32) / g);      // scalar
+        f16x4 s4[NT], z4[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          s4[t] = *at_bytes<f16x4>(S, (gi * (uint32_t)N + coff[t]) * 2u);
+          if constexpr (INT4) z4[t] = *at_bytes<f16x4>(Z, (gi * (uint32_t)N + coff[t]) * 2u);
+        }
+        f32x4 grp[MT][NT][4];
+#pragma unroll
+        for (int i = f * FL; i < (f + 1) * FL; ++i) {
+#pragma unroll
+          for (int t = 0; t < NT; ++t) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              f16x8 b;
+              if constexpr (INT4) {
+                const f16 nz = -clamp_zero(z4[t][j]);
+                b = raw_u4_word(w[i][t][j], f16x2{nz, nz});
+              } else {
+                b = raw_fp4_word(w[i][t][j]);
+              }
+#pragma unroll
+              for (int mt = 0; mt < MT; ++mt)
+                grp[mt][t][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    a[i][mt], b, i == f * FL ? f32x4{0, 0, 0, 0} : grp[mt][t][j], 0, 0, 0);
+            }
+          }
+        }
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const float sc = (float)sanitize_scale(s4[t][j]);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) acc[mt][t][j] += sc * grp[mt][t][j];
+          }
       }
     }
   }
 }
 
-// Tree-reduce the NW waves' accumulators through LDS (NW/2 tile buffers);
-// on return wave 0 holds the block sum.  NW must be a power of two.
+// Every wave but wave 0 parks its accumulators in LDS ((NW-1) tiles), one
+// barrier, then wave 0 adds them in wave order (deterministic).  On return
+// wave 0 holds the block sum; the other waves' values are unspecified.
 template <int MT, int NT, int NW>
 MM_DEV void skinny_block_reduce(float* red, f32x4 (&acc)[MT][NT][4]) {
   constexpr int TILE = MT * NT * 16 * 64;   // floats per wave: 16 per lane per (mt, t)
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (wave > 0) {
+    float* dst = red + (size_t)(wave - 1) * TILE;
 #pragma unroll
-  for (int half = NW / 2; half >= 1; half /= 2) {
-    if (wave >= half && wave < 2 * half) {
-      float* dst = red + (size_t)(wave - half) * TILE;
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
+      for (int t = 0; t < NT; ++t)
 #pragma unroll
-        for (int t = 0; t < NT; ++t)
+        for (int j = 0; j < 4; ++j)
+          *(f32x4*)(dst + (((mt * NT + t) * 4 + j) * 64 + lane) * 4) = acc[mt][t][j];
+  }
+  __syncthreads();
+  if (wave == 0) {
 #pragma unroll
-          for (int j = 0; j < 4; ++j)
-            *(f32x4*)(dst + (((mt * NT + t) * 4 + j) * 64 + lane) * 4) = acc[mt][t][j];
-    }
-    __syncthreads();
-    if (wave < half) {
-      const float* src = red + (size_t)wave * TILE;
+    for (int w = 0; w < NW - 1; ++w) {
+      const float* src = red + (size_t)w * TILE;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -129,8 +211,16 @@ MM_DEV void skinny_block_reduce(float* red, f32x4 (&acc)[MT][NT][4]) {
           for (int j = 0; j < 4; ++j)
             acc[mt][t][j] += *(const f32x4*)(src + (((mt * NT + t) * 4 + j) * 64 + lane) * 4);
     }
-    __syncthreads();
   }
+}
+
+// Steps per scale flush for a group size: g/32 capped at SPW when g is a
+// multiple of 32 and g/32 is a power of two or a multiple of SPW; else 0.
+inline int flush_steps(int g, int spw) {
+  if (g % 32 != 0) return 0;
+  const int gs = g / 32;
+  if (gs >= spw) return gs % spw == 0 ? spw : 0;
+  return (gs & (gs - 1)) == 0 ? gs : 0;
 }
 
 }  // namespace mmsk
