@@ -144,6 +144,35 @@ k_skinny(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
 
 
 
+
+// Column-strip kernel (M <= 16, group size a multiple of 32): one block per
+// NS*16 columns over the whole K; no split-K and no workspace.
+template <bool INT4, int NS, int SPW, int NW, int FL>
+__global__ void __launch_bounds__(NW * 64)
+k_strip(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
+        const f16* __restrict__ S, const f16* __restrict__ Z, f16* __restrict__ C, int ldc,
+        int M, int N, int K, int g, int nrounds) {
+  __shared__ float red[(NW - 1) * NS * 4 * 64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n0 = xcd_strip(blockIdx.x, gridDim.x) * 16 * NS;
+  f32x4 acc[NS];
+#pragma unroll
+  for (int t = 0; t < NS; ++t) acc[t] = f32x4{0, 0, 0, 0};
+  strip_wave<INT4, NS, SPW, FL>(A, lda, nullptr, 1, M, B, S, Z, N, K, g, n0, wave * SPW,
+                                nrounds, NW * SPW, acc);
+  strip_block_reduce<NS, NW>(red, acc);
+  if (wave != 0) return;
+  const int m = lane & 15, kb = lane >> 4;
+  if (m >= M) return;
+#pragma unroll
+  for (int t = 0; t < NS; ++t) {
+    const int col = n0 + 16 * t + 4 * kb;
+    if (col < N)
+      *(f16x4*)(C + (size_t)m * ldc + col) =
+          f16x4{(f16)acc[t][0], (f16)acc[t][1], (f16)acc[t][2], (f16)acc[t][3]};
+  }
+}
+
 // ===========================================================================
 // Prefill path
 // ===========================================================================
@@ -306,7 +335,7 @@ template <bool INT4, int WM, int WN, int RB, int CW, bool G64>
 __global__ void __launch_bounds__(WM * WN * 64)
 k_prefill2(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
            const f16* __restrict__ S, const f16* __restrict__ Z, f16* __restrict__ C, int ldc,
-           int M, int N, int K, int g) {
+           int M, int N, int K, int g, float* __restrict__ part) {
   // Wave tile: (32*RB) rows x (32*CW) columns; lane l32 owns CW adjacent
   // columns (CW packed words of one word row feed CW column tiles).
   // Requires K % 64 == 0 and N % 8 == 0 (checked by the host).
@@ -335,7 +364,13 @@ k_prefill2(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
   const int wm = wave / WN, wn = wave % WN;
   const int l32 = lane & 31, h = lane >> 5;
   const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-  const int nch = K / PF2_BK;
+  // K split: blockIdx.z owns chunks [c_beg, c_end); with gridDim.z > 1 the
+  // tile is written as an fp32 partial to part[z][M][N] instead of C.
+  const int nch_all = K / PF2_BK;
+  const int cps = (nch_all + gridDim.z - 1) / gridDim.z;
+  const int c_beg = blockIdx.z * cps;
+  const int c_end = min(nch_all, c_beg + cps);
+  const int nch = c_end;
   const int ngroups = K / g;
 
   // A piece (r, c8) lives at r*8 + (c8 ^ ((r >> 1) & 7)): 16 consecutive rows
@@ -394,7 +429,7 @@ k_prefill2(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
       for (int v = 0; v < 16; ++v) acc[rb][j][v] = 0.0f;
 
 #pragma unroll
-  for (int c = 0; c < PF2_STAGES - 1; ++c) issue(min(c, nch - 1), c);
+  for (int c = 0; c < PF2_STAGES - 1; ++c) issue(min(c_beg + c, nch - 1), c);
 
   // Per-lane LDS byte offsets, fixed for the whole K loop.
   const int colw = wn * 32 * CW + CW * l32;          // lane's first column within the tile
@@ -412,9 +447,15 @@ k_prefill2(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
     // Chunk ch's loads are complete once at most (STAGES-2) later chunks' loads
     // are outstanding; the barrier then publishes every thread's pieces and
     // guarantees the stage refilled below has been consumed by all waves.
+#ifndef MM_EXP_NOLOAD
     wait_vmcnt<(PF2_STAGES - 2) * LOADS_PER_CHUNK>();
+#endif
+#ifndef MM_EXP_NOBARRIER
     __builtin_amdgcn_s_barrier();
+#endif
+#ifndef MM_EXP_NOLOAD
     issue(min(ch + PF2_STAGES - 1, nch - 1), (st + PF2_STAGES - 1) % PF2_STAGES);
+#endif
     const int k0 = ch * PF2_BK;
     const int gi0 = k0 / g;
     f16x8 af[2][RB];
@@ -441,15 +482,17 @@ k_prefill2(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
         sv[slot] = *(const svec*)(smem + S_OFF + st * S_BYTES + so);
         if constexpr (INT4) zv[slot] = *(const svec*)(smem + Z_OFF + st * S_BYTES + so);
       }
+#ifdef MM_EXP_NOALDS
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+        af[slot][rb] = __builtin_bit_cast(f16x8, u32x4{a_off[t], a_off[t] + rb, 7u, 9u});
+#else
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb)
         af[slot][rb] = *(const f16x8*)(smem + a_off[t] + st * A_BYTES + rb * 32 * 128);
+#endif
     };
-    frag(0, 0);
-#pragma unroll
-    for (int t = 0; t < PF2_BK / 16; ++t) {
-      const int cur = t & 1;
-      f16x8 b[CW];
+    auto decode = [&](int slot, f16x8 (&b)[CW]) {
 #pragma unroll
       for (int j = 0; j < CW; ++j) {
         f16 nz = 0, sj;
@@ -457,22 +500,46 @@ k_prefill2(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
           sj = sc[j];
           if constexpr (INT4) nz = nzc[j];
         } else {
-          sj = sanitize_scale(sv[cur][j]);
-          if constexpr (INT4) nz = -clamp_zero(zv[cur][j]);
+          sj = sanitize_scale(sv[slot][j]);
+          if constexpr (INT4) nz = -clamp_zero(zv[slot][j]);
         }
-        b[j] = WordDq<INT4>::run(wv[cur][j], sj, nz);
+#ifdef MM_EXP_NODECODE
+        b[j] = __builtin_bit_cast(f16x8, u32x4{wv[slot][j], wv[slot][j] ^ 1u, wv[slot][j] ^ 2u, wv[slot][j] ^ 3u});
+#else
+        b[j] = WordDq<INT4>::run(wv[slot][j], sj, nz);
+#endif
       }
+    };
+    // Software pipeline: step t+1's fragments are read and decoded while
+    // step t's MFMAs occupy the matrix pipe.
+    frag(0, 0);
+    f16x8 bq[2][CW];
+    decode(0, bq[0]);
+#pragma unroll
+    for (int t = 0; t < PF2_BK / 16; ++t) {
+      const int cur = t & 1;
       if (t + 1 < PF2_BK / 16) frag(t + 1, cur ^ 1);
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
         for (int j = 0; j < CW; ++j)
           acc[rb][j] =
-              __builtin_amdgcn_mfma_f32_32x32x16_f16(af[cur][rb], b[j], acc[rb][j], 0, 0, 0);
+              __builtin_amdgcn_mfma_f32_32x32x16_f16(af[cur][rb], bq[cur][j], acc[rb][j], 0, 0, 0);
+      if (t + 1 < PF2_BK / 16) decode(cur ^ 1, bq[cur ^ 1]);
+#ifndef MM_PF2_NOSCHED
+      // Interleave each MFMA with a share of the next step's LDS reads and
+      // decode VALU so the matrix pipe never drains while they issue.
+#pragma unroll
+      for (int i = 0; i < RB * CW; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
+        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);   // VALU
+      }
+#endif
     }
   };
   static_assert(PF2_STAGES == 3, "chunk loop is unrolled for three stages");
-  for (int ch = 0; ch < nch; ch += 3) {
+  for (int ch = c_beg; ch < nch; ch += 3) {
     chunk(ch, std::integral_constant<int, 0>{});
     if (ch + 1 < nch) chunk(ch + 1, std::integral_constant<int, 1>{});
     if (ch + 2 < nch) chunk(ch + 2, std::integral_constant<int, 2>{});
@@ -481,19 +548,40 @@ k_prefill2(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
 
   const int ncol = n0 + colw;
   if (ncol >= N) return;
+  typedef float fvec __attribute__((ext_vector_type(CW)));
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
       const int row = m0 + wm * 32 * RB + rb * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
       if (row < M) {
-        svec o;
+        if (gridDim.z == 1) {
+          svec o;
 #pragma unroll
-        for (int j = 0; j < CW; ++j) o[j] = (f16)acc[rb][j][v];
-        *(svec*)(C + (size_t)row * ldc + ncol) = o;
+          for (int j = 0; j < CW; ++j) o[j] = (f16)acc[rb][j][v];
+          *(svec*)(C + (size_t)row * ldc + ncol) = o;
+        } else {
+          fvec o;
+#pragma unroll
+          for (int j = 0; j < CW; ++j) o[j] = acc[rb][j][v];
+          *(fvec*)(part + ((size_t)blockIdx.z * M + row) * N + ncol) = o;
+        }
       }
     }
   }
+}
+
+// Sum the K-split partials of the prefill kernel in split order -> fp16 C.
+__global__ void __launch_bounds__(256)
+k_splitk_reduce(const float* __restrict__ part, int ks, int M, int N, f16* __restrict__ C,
+                int ldc) {
+  const size_t i4 = (size_t)blockIdx.x * 256 + threadIdx.x;     // 4-column item
+  const size_t items = (size_t)M * (N / 4);
+  if (i4 >= items) return;
+  const int row = (int)(i4 / (N / 4)), col = 4 * (int)(i4 % (N / 4));
+  f32x4 v = {0, 0, 0, 0};
+  for (int z = 0; z < ks; ++z) v += *(const f32x4*)(part + ((size_t)z * M + row) * N + col);
+  *(f16x4*)(C + (size_t)row * ldc + col) = f16x4{(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
 }
 
 // ===========================================================================
@@ -593,6 +681,39 @@ int launch_skinny(const f16* A, int lda, const uint32_t* B, const f16* S, const 
 
 
 
+
+#ifndef MM_ST_NW
+#define MM_ST_NW 8
+#endif
+#ifndef MM_ST_SPW
+#define MM_ST_SPW 8
+#endif
+#ifndef MM_ST_MODE
+#define MM_ST_MODE 1        // 0: never, 1: heuristic, 2: always (M <= 16, g % 32 == 0)
+#endif
+
+template <bool INT4, int NS>
+int launch_strip(const f16* A, int lda, const uint32_t* B, const f16* S, const f16* Z, f16* C,
+                 int ldc, int M, int N, int K, int g, hipStream_t st) {
+  constexpr int NW = MM_ST_NW, SPW = MM_ST_SPW;
+  const int nsl = (K / 8 + 3) / 4;
+  const int nrounds = mm_cdiv(nsl, NW * SPW);
+  const int fl = flush_steps(g, SPW);
+#define MM_LAUNCH_ST(FLV)                                                                     \
+  hipLaunchKernelGGL((k_strip<INT4, NS, SPW, NW, FLV>), dim3(mm_cdiv(N, 16 * NS)), dim3(NW * 64), \
+                     0, st, A, lda, B, S, Z, C, ldc, M, N, K, g, nrounds)
+  switch (fl) {
+    case 1: MM_LAUNCH_ST(1); break;
+    case 2: MM_LAUNCH_ST(2); break;
+    case 4: MM_LAUNCH_ST(4); break;
+    case 8: MM_LAUNCH_ST(8 <= SPW ? 8 : 4); break;
+    default: MM_CHECK_ARG(false, "gemm(strip): unsupported group size %d", g);
+  }
+#undef MM_LAUNCH_ST
+  MM_CHECK_LAUNCH("gemm(strip)");
+  return 0;
+}
+
 template <bool INT4, int WM, int WN, int RB>
 int launch_prefill(const f16* A, int lda, const uint32_t* B, const f16* S, const f16* Z, f16* C,
                    int ldc, int M, int N, int K, int g, hipStream_t st) {
@@ -619,18 +740,50 @@ int launch_prefill(const f16* A, int lda, const uint32_t* B, const f16* S, const
 #define PF2_SMALL 1, 4, 2, 2     // 64 x 256, 4 waves of 64 x 64
 #endif
 
+// Prefill plan: tile config (0: 256x256, 1: 128x256, 2: 64x256) and K split.
+struct PrefillPlan {
+  int cfg;
+  int ksplit;
+};
+
+PrefillPlan plan_prefill(int M, int N, int K) {
+  PrefillPlan p;
+  static const int BMs[3] = {256, 128, 64};
+  const long t256 = (long)mm_cdiv(M, 256) * mm_cdiv(N, 256);
+  p.cfg = (M > 128 && t256 >= 240) ? 0 : (M > 64 ? 1 : 2);
+  const long blocks = (long)mm_cdiv(M, BMs[p.cfg]) * mm_cdiv(N, 256);
+  // Split K when the grid cannot fill the 256 CUs; every split keeps >= 8
+  // chunks of 64 k so the pipeline stays full.
+  const int nch = K / PF2_BK;
+  int ks = 1;
+  while (blocks * ks < 200 && nch / (ks * 2) >= 8) ks *= 2;
+  p.ksplit = ks;
+  return p;
+}
+
+size_t prefill_ws_bytes(int M, int N, int K) {
+  const PrefillPlan p = plan_prefill(M, N, K);
+  return p.ksplit > 1 ? (size_t)p.ksplit * M * N * sizeof(float) : 0;
+}
+
 template <bool INT4, int WM, int WN, int RB, int CW>
 int launch_prefill2(const f16* A, int lda, const uint32_t* B, const f16* S, const f16* Z, f16* C,
-                    int ldc, int M, int N, int K, int g, hipStream_t st) {
+                    int ldc, int M, int N, int K, int g, int ks, float* part, hipStream_t st) {
   constexpr int BM = WM * 32 * RB, BN = WN * 32 * CW;
-  dim3 grid(mm_cdiv(N, BN), mm_cdiv(M, BM));
+  dim3 grid(mm_cdiv(N, BN), mm_cdiv(M, BM), ks);
   if (g % PF2_BK == 0)
     hipLaunchKernelGGL((k_prefill2<INT4, WM, WN, RB, CW, true>), grid, dim3(WM * WN * 64), 0, st,
-                       A, lda, B, S, Z, C, ldc, M, N, K, g);
+                       A, lda, B, S, Z, C, ldc, M, N, K, g, part);
   else
     hipLaunchKernelGGL((k_prefill2<INT4, WM, WN, RB, CW, false>), grid, dim3(WM * WN * 64), 0, st,
-                       A, lda, B, S, Z, C, ldc, M, N, K, g);
+                       A, lda, B, S, Z, C, ldc, M, N, K, g, part);
   MM_CHECK_LAUNCH("gemm(prefill2)");
+  if (ks > 1) {
+    const size_t items = (size_t)M * (N / 4);
+    hipLaunchKernelGGL(k_splitk_reduce, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, st,
+                       part, ks, M, N, C, ldc);
+    MM_CHECK_LAUNCH("gemm(prefill split-K reduce)");
+  }
   return 0;
 }
 
@@ -647,16 +800,36 @@ int gemm_dispatch(const char* who, const f16* A, const uint32_t* B, const f16* S
                    ((uintptr_t)C & 7) == 0 && (!INT4 || ((uintptr_t)Z & 7) == 0),
                "%s: operands must be 16-byte (A, B) / 8-byte (scales, zeros, C) aligned", who);
   if (M == 0) return 0;
+  if (MM_ST_MODE && M <= 16 && flush_steps(g, MM_ST_SPW) > 0) {
+    // Column strips (no split-K hand-off) win for small layers, where the
+    // hand-off is a large share of the launch; split-K wins from ~13 MB up
+    // (measured on MI355X: 4096x4096 5.8 vs 7.0 us, 4096x6144 8.0 vs 7.2 us).
+    if (MM_ST_MODE == 2 || ((long)K * N <= 4096L * 4096 && N / 16 >= 128))
+      return launch_strip<INT4, 1>(A, K, B, S, Z, C, N, M, N, K, g, st);
+  }
   if (M <= 16) return launch_skinny<INT4, 1>(A, K, B, S, Z, C, N, M, N, K, g, ws, ws_bytes, st);
   if (M <= 32) return launch_skinny<INT4, 2>(A, K, B, S, Z, C, N, M, N, K, g, ws, ws_bytes, st);
   // The pipelined kernel stages scale rows in 8-column pieces (N % 8 == 0)
   // and whole 64-k chunks (K % 64 == 0).
   if (MM_PF2_ENABLE && N % 8 == 0 && K % PF2_BK == 0) {
-    const long t256 = (long)mm_cdiv(M, 256) * mm_cdiv(N, 256);
-    if (M > 128 && t256 >= 240)
-      return launch_prefill2<INT4, PF2_BIG>(A, K, B, S, Z, C, N, M, N, K, g, st);
-    if (M > 64) return launch_prefill2<INT4, PF2_MID>(A, K, B, S, Z, C, N, M, N, K, g, st);
-    return launch_prefill2<INT4, PF2_SMALL>(A, K, B, S, Z, C, N, M, N, K, g, st);
+    const PrefillPlan p = plan_prefill(M, N, K);
+    float* part = nullptr;
+    if (p.ksplit > 1) {
+      const size_t need = SK_COUNTER_BYTES + prefill_ws_bytes(M, N, K);
+      MM_CHECK_ARG(ws != nullptr && ws_bytes >= need,
+                   "%s: workspace of %zu bytes is smaller than the %zu required", who, ws_bytes,
+                   need);
+      part = (float*)((char*)ws + SK_COUNTER_BYTES);
+    }
+    switch (p.cfg) {
+      case 0:
+        return launch_prefill2<INT4, PF2_BIG>(A, K, B, S, Z, C, N, M, N, K, g, p.ksplit, part, st);
+      case 1:
+        return launch_prefill2<INT4, PF2_MID>(A, K, B, S, Z, C, N, M, N, K, g, p.ksplit, part, st);
+      default:
+        return launch_prefill2<INT4, PF2_SMALL>(A, K, B, S, Z, C, N, M, N, K, g, p.ksplit, part,
+                                                st);
+    }
   }
   // Prefill tiles: the largest tile that still gives about one block per CU.
   const long t256 = (long)mm_cdiv(M, 256) * mm_cdiv(N, 256);
@@ -672,7 +845,8 @@ int gemm_dispatch(const char* who, const f16* A, const uint32_t* B, const f16* S
 // C ABI
 // ===========================================================================
 extern "C" size_t mm_gemm_workspace_bytes(int M, int N, int K) {
-  if (M <= 0 || N <= 0 || K <= 0 || M > 32) return SK_COUNTER_BYTES;
+  if (M <= 0 || N <= 0 || K <= 0) return SK_COUNTER_BYTES;
+  if (M > 32) return SK_COUNTER_BYTES + prefill_ws_bytes(M, N, K);
   return skinny_ws_bytes(M, N, K);
 }
 

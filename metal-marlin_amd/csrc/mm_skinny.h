@@ -214,6 +214,137 @@ MM_DEV void skinny_block_reduce(float* red, f32x4 (&acc)[MT][NT][4]) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Column-strip core (M <= 16, g % 32 == 0; no split-K).  The weights are the
+// MFMA A operand and the activations the B operand, so one MFMA 16x16x32
+// consumes one packed word per lane:
+//   lane l = 16*kb + i at slab sl (4 word rows = 32 k): weight word
+//   (kp = 4*sl + kb, column n0 + 16*t + i) -- 16 lanes read 64 contiguous
+//   bytes of a word row -- and activation row min(i, M-1), k = 8*kp .. +7.
+//   D tile t: lane holds columns n0 + 16*t + 4*kb + r (r = 0..3), row m = i.
+// Wave w takes slabs w*SPW + r*slstride + u.  Rounds are software-pipelined:
+// round r+1's loads are issued before round r's math.
+// ---------------------------------------------------------------------------
+template <int NS, int SPW>
+struct StripRound {
+  uint32_t w[SPW][NS];
+  f16x8 a[SPW];
+};
+
+template <bool INT4, int NS, int SPW, int FL>
+MM_DEV void strip_wave(const f16* __restrict__ A, int lda, const int* __restrict__ rowmap,
+                       int rowdiv, int M, const uint32_t* __restrict__ B,
+                       const f16* __restrict__ S, const f16* __restrict__ Z, int N, int K, int g,
+                       int n0, int sl0, int nrounds, int slstride, f32x4 (&acc)[NS]) {
+  static_assert(FL > 0 && SPW % FL == 0, "strip path needs a post-scale flush interval");
+  const int lane = threadIdx.x & 63;
+  const int i = lane & 15, kb = lane >> 4;
+  const int KP = K >> 3;
+  const int nsl = (KP + 3) >> 2;
+  const int m = min(i, M - 1);
+  const uint32_t aoff = (uint32_t)(rowmap != nullptr ? rowmap[m] / rowdiv : m) *
+                        (uint32_t)lda * 2u;
+  uint32_t bcol[NS], scol[NS];
+#pragma unroll
+  for (int t = 0; t < NS; ++t) {
+    bcol[t] = (uint32_t)min(n0 + 16 * t + i, N - 1);           // weight column
+    scol[t] = (uint32_t)min(n0 + 16 * t + 4 * kb, N - 4);      // output columns
+  }
+  auto load = [&](int r, StripRound<NS, SPW>& R) {
+    const int slb = sl0 + r * slstride;
+#pragma unroll
+    for (int u = 0; u < SPW; ++u) {
+      const int kp = min(4 * min(slb + u, nsl - 1) + kb, KP - 1);
+#pragma unroll
+      for (int t = 0; t < NS; ++t)
+        R.w[u][t] = *at_bytes<uint32_t>(B, ((uint32_t)kp * (uint32_t)N + bcol[t]) * 4u);
+      R.a[u] = *at_bytes<f16x8>(A, aoff + (uint32_t)kp * 16u);
+    }
+  };
+  auto math = [&](int r, StripRound<NS, SPW>& R) {
+    const int slb = sl0 + r * slstride;
+    if (slb + SPW > nsl) {
+#pragma unroll
+      for (int u = 0; u < SPW; ++u)
+        if (slb + u >= nsl) R.a[u] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int f = 0; f < SPW / FL; ++f) {
+      const int slg = min(slb + f * FL, nsl - 1);
+      const uint32_t gi = (uint32_t)((slg * 32) / g);
+      f16x4 s4[NS];
+      f16 zc[NS];
+#pragma unroll
+      for (int t = 0; t < NS; ++t) {
+        s4[t] = *at_bytes<f16x4>(S, (gi * (uint32_t)N + scol[t]) * 2u);
+        if constexpr (INT4) zc[t] = *at_bytes<f16>(Z, (gi * (uint32_t)N + bcol[t]) * 2u);
+      }
+      f32x4 grp[NS];
+#pragma unroll
+      for (int u = f * FL; u < (f + 1) * FL; ++u) {
+#pragma unroll
+        for (int t = 0; t < NS; ++t) {
+          f16x8 b;
+          if constexpr (INT4) {
+            const f16 nz = -clamp_zero(zc[t]);
+            b = raw_u4_word(R.w[u][t], f16x2{nz, nz});
+          } else {
+            b = raw_fp4_word(R.w[u][t]);
+          }
+          grp[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+              b, R.a[u], u == f * FL ? f32x4{0, 0, 0, 0} : grp[t], 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < NS; ++t)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr)
+          acc[t][rr] += (float)sanitize_scale(s4[t][rr]) * grp[t][rr];
+    }
+  };
+  // Rounds whose first slab is past the end are skipped (wave-uniform).
+  int nr = 0;
+  while (nr < nrounds && sl0 + nr * slstride < nsl) ++nr;
+  if (nr == 0) return;
+  StripRound<NS, SPW> R0, R1;
+  load(0, R0);
+  for (int r = 0; r < nr; r += 2) {
+    if (r + 1 < nr) load(r + 1, R1);
+    math(r, R0);
+    if (r + 1 >= nr) break;
+    if (r + 2 < nr) load(r + 2, R0);
+    math(r + 1, R1);
+  }
+}
+
+// Every wave but wave 0 parks its accumulators in LDS, one barrier, then
+// wave 0 adds them in wave order (deterministic).
+template <int NS, int NW>
+MM_DEV void strip_block_reduce(float* red, f32x4 (&acc)[NS]) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (wave > 0) {
+#pragma unroll
+    for (int t = 0; t < NS; ++t)
+      *(f32x4*)(red + (((size_t)(wave - 1) * NS + t) * 64 + lane) * 4) = acc[t];
+  }
+  __syncthreads();
+  if (wave == 0) {
+#pragma unroll
+    for (int w = 0; w < NW - 1; ++w)
+#pragma unroll
+      for (int t = 0; t < NS; ++t)
+        acc[t] += *(const f32x4*)(red + (((size_t)w * NS + t) * 64 + lane) * 4);
+  }
+}
+
+// Block -> strip index keeping neighbouring strips on one XCD (blocks are
+// dealt round-robin to the 8 XCDs, each with its own L2), so both 64-byte
+// halves of a 128-byte line are fetched into the same L2.
+MM_DEV int xcd_strip(int bid, int nblk) {
+  if (nblk % 8 != 0) return bid;
+  return (bid % 8) * (nblk / 8) + bid / 8;
+}
+
 // Steps per scale flush for a group size: g/32 capped at SPW when g is a
 // multiple of 32 and g/32 is a power of two or a multiple of SPW; else 0.
 inline int flush_steps(int g, int spw) {
