@@ -145,6 +145,59 @@ def run_prefill_bench(torch, mmfp4, M: int, steps: int, warmup: int):
             "launch_us_avg": 1e3 * total_ms / (steps * len(PREFILL))}
 
 
+def run_single_bench(torch, mmfp4, M: int, K: int, N: int, steps: int):
+    """One FP4 linear (config 1: M=1, 4096 -> 4096), rotated weight copies."""
+    copies = max(2, -(-ROTATE_BYTES // alg_bytes(0, K, N)))
+    ws = [make_weights(torch, mmfp4, K, N, 500 + c) for c in range(copies)]
+    a = torch.randn((M, K), device="cuda").half()
+    launches = [[lambda w=w: mmfp4.marlin_gemm_fp4(a, w[0], w[1], G)] for w in ws]
+    ms = timed_launches(torch, launches, steps, 10)
+    us = 1e3 * ms / steps
+    return {"M": M, "K": K, "N": N, "us": round(us, 3),
+            "TBps": round(alg_bytes(M, K, N) / (us * 1e-6) / 1e12, 3)}
+
+
+MOE = {"E": 128, "H": 2048, "I": 768, "k": 8}
+
+
+def run_moe_bench(torch, mmfp4, T: int, steps: int):
+    """Qwen3-30B-A3B routed experts (config 5): sort -> gate_up (+SwiGLU) ->
+    down -> combine, four launches, all 128 experts resident; router logits
+    N(0,1) seed 2, fp32 softmax -> top-8 -> renormalise.  Two copies of the
+    expert weights (622 MB) are rotated so each step reads HBM."""
+    E, H, I, k = MOE["E"], MOE["H"], MOE["I"], MOE["k"]
+    sets = []
+    for c in range(2):
+        gen = torch.Generator(device="cuda").manual_seed(600 + c)
+        gu_p = torch.empty((E, H // 8, 2 * I), dtype=torch.int32, device="cuda")
+        gu_s = torch.empty((E, H // G, 2 * I), dtype=torch.float16, device="cuda")
+        dn_p = torch.empty((E, I // 8, H), dtype=torch.int32, device="cuda")
+        dn_s = torch.empty((E, I // G, H), dtype=torch.float16, device="cuda")
+        for e in range(E):
+            w = (torch.randn((2 * I, H), generator=gen, device="cuda") * 0.02).half()
+            gu_p[e], gu_s[e] = mmfp4.quantize_fp4(w, group_size=G)
+            w = (torch.randn((H, I), generator=gen, device="cuda") * 0.02).half()
+            dn_p[e], dn_s[e] = mmfp4.quantize_fp4(w, group_size=G)
+        sets.append((gu_p, gu_s, dn_p, dn_s))
+    gen = torch.Generator(device="cuda").manual_seed(2)
+    logits = torch.randn((T, E), generator=gen, device="cuda")
+    probs = torch.softmax(logits.float(), dim=-1)
+    topw, ids = torch.topk(probs, k, dim=-1)
+    topw = topw / topw.sum(dim=-1, keepdim=True)
+    x = torch.randn((T, H), generator=gen, device="cuda").half()
+    used = int(torch.unique(ids).numel())
+    launches = [[lambda s=s: mmfp4.moe_mlp_fp4(x, s[0], s[1], s[2], s[3], ids, topw, G)]
+                for s in sets]
+    ms = timed_launches(torch, launches, steps, 4)
+    us = 1e3 * ms / steps
+    per_expert = (H * 2 * I // 2 + 2 * 2 * I * (H // G)) + (I * H // 2 + 2 * H * (I // G))
+    byts = used * per_expert + 2 * T * H * 2 + 2 * (T * k) * I * 2
+    flops = 9437184 * T * k
+    return {"T": T, "experts_hit": used, "us": round(us, 2),
+            "TBps": round(byts / (us * 1e-6) / 1e12, 3),
+            "TFLOPs": round(flops / (us * 1e-6) / 1e12, 1), "algorithmic_bytes": byts}
+
+
 def measured_traffic(name: str) -> float | None:
     """HBM bytes per launch from the committed rocprofv3 --pmc summary (FETCH_SIZE
     and WRITE_SIZE runs of `bench.py --pmc-probe`, calibrated on a known copy)."""
@@ -284,6 +337,8 @@ def main() -> int:
                           FP16_PEAK_TFLOPS, 4), "ms_per_step": round(pre["ms_per_step"], 4),
                           "per_shape": pre["per_shape"], "kernel": "k_prefill (MFMA 32x32x16)"},
     }
+    out["config1_single_linear_m1"] = run_single_bench(torch, mmfp4, 1, 4096, 4096, 100)
+    out["config5_moe_qwen3_30b_a3b"] = [run_moe_bench(torch, mmfp4, T, 20) for T in (32, 1024)]
     if args.all:
         extra = {}
         for M in (8, 32):

@@ -447,15 +447,9 @@ k_prefill2(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
     // Chunk ch's loads are complete once at most (STAGES-2) later chunks' loads
     // are outstanding; the barrier then publishes every thread's pieces and
     // guarantees the stage refilled below has been consumed by all waves.
-#ifndef MM_EXP_NOLOAD
     wait_vmcnt<(PF2_STAGES - 2) * LOADS_PER_CHUNK>();
-#endif
-#ifndef MM_EXP_NOBARRIER
     __builtin_amdgcn_s_barrier();
-#endif
-#ifndef MM_EXP_NOLOAD
     issue(min(ch + PF2_STAGES - 1, nch - 1), (st + PF2_STAGES - 1) % PF2_STAGES);
-#endif
     const int k0 = ch * PF2_BK;
     const int gi0 = k0 / g;
     f16x8 af[2][RB];
@@ -482,15 +476,9 @@ k_prefill2(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
         sv[slot] = *(const svec*)(smem + S_OFF + st * S_BYTES + so);
         if constexpr (INT4) zv[slot] = *(const svec*)(smem + Z_OFF + st * S_BYTES + so);
       }
-#ifdef MM_EXP_NOALDS
-#pragma unroll
-      for (int rb = 0; rb < RB; ++rb)
-        af[slot][rb] = __builtin_bit_cast(f16x8, u32x4{a_off[t], a_off[t] + rb, 7u, 9u});
-#else
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb)
         af[slot][rb] = *(const f16x8*)(smem + a_off[t] + st * A_BYTES + rb * 32 * 128);
-#endif
     };
     auto decode = [&](int slot, f16x8 (&b)[CW]) {
 #pragma unroll
@@ -503,11 +491,7 @@ k_prefill2(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
           sj = sanitize_scale(sv[slot][j]);
           if constexpr (INT4) nz = -clamp_zero(zv[slot][j]);
         }
-#ifdef MM_EXP_NODECODE
-        b[j] = __builtin_bit_cast(f16x8, u32x4{wv[slot][j], wv[slot][j] ^ 1u, wv[slot][j] ^ 2u, wv[slot][j] ^ 3u});
-#else
         b[j] = WordDq<INT4>::run(wv[slot][j], sj, nz);
-#endif
       }
     };
     // Software pipeline: step t+1's fragments are read and decoded while
@@ -526,7 +510,6 @@ k_prefill2(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
           acc[rb][j] =
               __builtin_amdgcn_mfma_f32_32x32x16_f16(af[cur][rb], bq[cur][j], acc[rb][j], 0, 0, 0);
       if (t + 1 < PF2_BK / 16) decode(cur ^ 1, bq[cur ^ 1]);
-#ifndef MM_PF2_NOSCHED
       // Interleave each MFMA with a share of the next step's LDS reads and
       // decode VALU so the matrix pipe never drains while they issue.
 #pragma unroll
@@ -535,7 +518,6 @@ k_prefill2(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
         __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);   // VALU
       }
-#endif
     }
   };
   static_assert(PF2_STAGES == 3, "chunk loop is unrolled for three stages");

@@ -99,16 +99,17 @@ k_moe_sort(const int32_t* __restrict__ ids, int n, int E, int32_t* __restrict__ 
 //   act == 0: NT=2 tiles of 64 columns at n0 and n0+64.
 //   act == 1: tile 0 = gate columns [n0, n0+64), tile 1 = up columns
 //             [N/2 + n0, ...); output silu(gate) * up, width N/2.
-constexpr int MOE_NW = 4;
-constexpr int MOE_SPW = 4;
-
-template <int MT, int FL>
-__global__ void __launch_bounds__(MOE_NW * 64)
+// NW waves split K, each taking SPW 32-k steps per round; the host picks
+// (NW, SPW) per launch from the expert's K so that few rounds remain and no
+// wave idles.
+template <int MT, int NW, int SPW, int FL>
+__global__ void __launch_bounds__(NW * 64)
 k_moe_grouped(const f16* __restrict__ X, const int32_t* __restrict__ sorted_idx,
               const int32_t* __restrict__ offsets, int gather, int topk,
               const uint32_t* __restrict__ Ball, const f16* __restrict__ Sall, int K, int N,
               int g, int act, f16* __restrict__ Y) {
   constexpr int NT = 2;
+  constexpr int MOE_NW = NW, MOE_SPW = SPW;
   __shared__ float red[(MOE_NW - 1) * MT * NT * 16 * 64];
   const int e = blockIdx.z;
   const int r0 = offsets[e], r1 = offsets[e + 1];
@@ -224,27 +225,34 @@ extern "C" int mm_moe_grouped_gemm(const uint16_t* X, const int32_t* sorted_idx,
   const int nout = act ? N / 2 : N;
   const int tiles = act ? mm_cdiv(nout, SK_COLS) : mm_cdiv(N, 2 * SK_COLS);
   dim3 grid(tiles, 1, E);
-  const int avg_rows = (T * k + E - 1) / E;
-  const int fl = flush_steps(g, MOE_SPW);
-#define MM_LAUNCH_MOE(MTV, FLV)                                                              \
-  hipLaunchKernelGGL((k_moe_grouped<MTV, FLV>), grid, dim3(MOE_NW * 64), 0, (hipStream_t)stream, \
-                     (const f16*)X, sorted_idx, offsets, gather, k, B, (const f16*)S, K, N, g,  \
-                     act, (f16*)Y)
-  if (avg_rows <= 16) {
-    switch (fl) {
-      case 1: MM_LAUNCH_MOE(1, 1); break;
-      case 2: MM_LAUNCH_MOE(1, 2); break;
-      case 4: MM_LAUNCH_MOE(1, 4); break;
-      default: MM_LAUNCH_MOE(1, 0); break;
-    }
-  } else {
-    switch (fl) {
-      case 1: MM_LAUNCH_MOE(2, 1); break;
-      case 2: MM_LAUNCH_MOE(2, 2); break;
-      case 4: MM_LAUNCH_MOE(2, 4); break;
-      default: MM_LAUNCH_MOE(2, 0); break;
-    }
+  // Blocks the launch can keep busy: column tiles x experts that can hold a
+  // row.  Few blocks (a handful of tokens): 8 waves x 8 steps per block so
+  // each block pulls more bytes; otherwise 4 waves x 4 steps, which keeps
+  // more blocks resident per CU (measured best from 8 to 8192 rows).
+  const long busy = (long)tiles * (long)std::min<long>(E, (long)T * k);
+#ifdef MM_MOE_FORCE
+  const int cfg = MM_MOE_FORCE;
+#else
+  const int cfg = busy < 512 ? 0 : 1;
+#endif
+#define MM_LAUNCH_MOE(MTV, NWV, SPWV, FLV)                                                     \
+  hipLaunchKernelGGL((k_moe_grouped<MTV, NWV, SPWV, FLV>), grid, dim3(NWV * 64), 0,               \
+                     (hipStream_t)stream, (const f16*)X, sorted_idx, offsets, gather, k, B,        \
+                     (const f16*)S, K, N, g, act, (f16*)Y)
+#define MM_LAUNCH_MOE_FL(MTV, NWV, SPWV)                                                       \
+  switch (flush_steps(g, SPWV)) {                                                              \
+    case 1: MM_LAUNCH_MOE(MTV, NWV, SPWV, 1); break;                                           \
+    case 2: MM_LAUNCH_MOE(MTV, NWV, SPWV, 2); break;                                           \
+    case 4: MM_LAUNCH_MOE(MTV, NWV, SPWV, 4); break;                                           \
+    case 8: MM_LAUNCH_MOE(MTV, NWV, SPWV, (SPWV % 8 == 0 ? 8 : 0)); break;                     \
+    default: MM_LAUNCH_MOE(MTV, NWV, SPWV, 0); break;                                          \
   }
+  if (cfg == 0) {
+    MM_LAUNCH_MOE_FL(1, 8, 8);
+  } else {
+    MM_LAUNCH_MOE_FL(1, 4, 4);
+  }
+#undef MM_LAUNCH_MOE_FL
 #undef MM_LAUNCH_MOE
   MM_CHECK_LAUNCH("mm_moe_grouped_gemm");
   return 0;
