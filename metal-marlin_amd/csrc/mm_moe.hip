@@ -12,11 +12,18 @@
 // writer and the combine sums the k slots in fixed order.
 #include "mm_common.h"
 #include "mm_skinny.h"
+#include "mm_prefill.h"
 
 namespace {
 using namespace mmsk;
+using namespace mmpf;
+
+#ifndef MM_MOE_PF_ROWS
+#define MM_MOE_PF_ROWS 24   // average rows per expert above which the MFMA tile kernel runs
+#endif
 
 constexpr int SORT_THREADS = 1024;
+constexpr int MOE_MAX_EXPERTS = SORT_THREADS;   // the sort holds one expert per thread
 constexpr int SORT_WAVES = SORT_THREADS / 64;
 
 // One block.  Dynamic LDS: cursor[E] + wcnt[SORT_WAVES][E] ints.
@@ -172,6 +179,124 @@ k_moe_grouped(const f16* __restrict__ X, const int32_t* __restrict__ sorted_idx,
   }
 }
 
+// ---------------------------------------------------------------------------
+// Grouped expert GEMM, prefill-sized groups: the pipelined MFMA main loop of
+// the dense prefill kernel (mm_prefill.h) over one (expert, row tile,
+// column tile) per block.  grid.y enumerates row tiles of BM rows over all
+// experts in expert order; each block finds its expert with one wave scan of
+// the offsets (grid.y is an upper bound; surplus blocks exit).  A rows are
+// gathered through sorted_idx (gather=1) or read in sorted order.  Column
+// map (tile-major, CW=2): each wave's 64 LDS columns are 32 output columns
+// twice -- act=1: the gate columns then the matching up columns (N/2 on),
+// so silu(gate)*up is formed in registers; act=0: 64 consecutive columns.
+// Row blocks of a wave that lie past the expert's rows skip their MFMAs.
+// ---------------------------------------------------------------------------
+struct MoeSrc {
+  const f16* X;
+  const int32_t* sidx;
+  int gather, topk, K;
+  int mb, rlast;           // first sorted row of the tile, last row of the expert
+  int act, half, o0;       // act=1: half = N/2, o0 = first output column
+  const uint32_t* B;
+  const f16* S;
+  const f16* Z;
+  int ld;
+  MM_DEV const f16* arow(int r) const {
+    const int sr = min(mb + r, rlast);
+    return X + (size_t)(gather ? sidx[sr] / topk : sr) * K;
+  }
+  MM_DEV int col(int P, int w) const {
+    if (!act) return min(o0 + P, ld - w);
+    const int oc = min(o0 + 32 * (P >> 6) + (P & 31), half - w);
+    return (P & 32) ? half + oc : oc;
+  }
+};
+
+template <int WM, int WN, int RB, bool G64>
+__global__ void __launch_bounds__(WM * WN * 64)
+k_moe_prefill(const f16* __restrict__ X, const int32_t* __restrict__ sorted_idx,
+              const int32_t* __restrict__ offsets, int gather, int topk,
+              const uint32_t* __restrict__ Ball, const f16* __restrict__ Sall, int E, int K,
+              int N, int g, int act, int gx, f16* __restrict__ Y) {
+  constexpr int CW = 2;
+  using Sh = Pf2Shape<false, WM, WN, RB, CW>;
+  constexpr int BM = Sh::BM, BN = Sh::BN;
+  __shared__ __attribute__((aligned(16))) char smem[Sh::LDS_BYTES];
+  __shared__ int tp[MOE_MAX_EXPERTS + 1];     // row-tile prefix over experts
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int l32 = lane & 31, h = lane >> 5;
+
+  // tp[e] = row tiles of experts < e (one wave scan).
+  if (wave == 0) {
+    int base = 0;
+    for (int e0 = 0; e0 < E; e0 += 64) {
+      const int e = e0 + lane;
+      const int t = e < E ? (offsets[e + 1] - offsets[e] + BM - 1) / BM : 0;
+      int incl = t;
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const int o = __shfl_up(incl, d);
+        if (lane >= d) incl += o;
+      }
+      if (e < E) tp[e + 1] = base + incl;
+      base += __shfl(incl, 63);
+    }
+    if (lane == 0) tp[0] = 0;
+  }
+  __syncthreads();
+  // The grid is an upper bound on gx * (row tiles); blocks past the real
+  // count exit.  Blocks are dealt round-robin to the 8 XCDs, so the linear id
+  // is remapped to give each XCD one contiguous run of (row tile, column
+  // tile) pairs: the column tiles of one row tile then share their A rows in
+  // that XCD's L2.
+  const int nreal = gx * tp[E];
+  const int L = blockIdx.x;
+  if (L >= nreal) return;
+  const int xcd = L & 7, q = nreal >> 3, rem = nreal & 7;
+  const int lin = xcd * q + min(xcd, rem) + (L >> 3);
+  const int y = lin / gx, bx = lin - y * gx;
+  int lo = 0, hi = E - 1;            // expert e with tp[e] <= y < tp[e + 1]
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (tp[mid] <= y) lo = mid; else hi = mid - 1;
+  }
+  const int e = lo;
+  const int r0 = offsets[e], r1 = offsets[e + 1];
+  const int mb = r0 + (y - tp[e]) * BM;
+  const int rows = min(BM, r1 - mb);
+  const int half = N / 2;
+  const int o0 = act ? bx * (BN / 2) : bx * BN;
+  const MoeSrc src{X, sorted_idx, gather, topk, K, mb, r1 - 1, act, half, o0,
+                   Ball + (size_t)e * (K / 8) * N, Sall + (size_t)e * (K / g) * N, nullptr, N};
+  const int rb_live =
+      __builtin_amdgcn_readfirstlane(min(RB, max(0, (rows - wm * 32 * RB + 31) / 32)));
+  f32x16 acc[RB][CW];
+  pf2_mainloop<false, WM, WN, RB, CW, G64, true>(src, K, g, 0, K / PF2_BK, rb_live, smem, acc);
+
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int r = wm * 32 * RB + rb * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+      if (r >= rows) continue;
+      if (act) {
+        const int oc = o0 + wn * 32 + l32;
+        if (oc < half) {
+          const float gt = acc[rb][0][v], up = acc[rb][1][v];
+          Y[(size_t)(mb + r) * half + oc] = (f16)(gt / (1.0f + __expf(-gt)) * up);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < CW; ++j) {
+          const int c = o0 + wn * 64 + 32 * j + l32;
+          if (c < N) Y[(size_t)(mb + r) * N + c] = (f16)acc[rb][j][v];
+        }
+      }
+    }
+  }
+}
+
 // out[t, :] = sum_j probs[t, j] * Y[inverse[t*k + j], :]; one block per token,
 // 8 columns per thread.
 __global__ void __launch_bounds__(256)
@@ -223,6 +348,46 @@ extern "C" int mm_moe_grouped_gemm(const uint16_t* X, const int32_t* sorted_idx,
                "mm_moe_grouped_gemm: N=%d must be divisible by %d", N, act ? 8 : 4);
   if (T == 0) return 0;
   const int nout = act ? N / 2 : N;
+  // Prefill-sized groups (more than MM_MOE_PF_ROWS rows per expert on
+  // average) run the MFMA tile kernel when the shapes allow its 16-byte
+  // pieces: K % 64 == 0, N % 8 == 0 (N % 16 == 0 with SwiGLU).
+  if ((long)T * k > (long)MM_MOE_PF_ROWS * E && K % PF2_BK == 0 && N % (act ? 16 : 8) == 0 &&
+      E <= MOE_MAX_EXPERTS) {
+    const long tk = (long)T * k;
+    // Row tile: 64 rows while groups average under 48 rows, else 96 (measured
+    // on MI355X at the Qwen3-30B-A3B shapes, T = 256..4096: 96-row tiles beat
+    // 128 and 256 once per-expert counts vary by tens of rows).
+#ifdef MM_MOE_PF_CFG
+    const int cfg = MM_MOE_PF_CFG;
+#else
+    const int cfg = tk < 48L * E ? 1 : 3;
+#endif
+#define MM_LAUNCH_MOE_PF(WM, WN, RB)                                                           \
+  do {                                                                                         \
+    constexpr int BM = WM * 32 * RB, BN = WN * 64;                                             \
+    const int gx = act ? mm_cdiv(nout, BN / 2) : mm_cdiv(N, BN);                               \
+    const long blocks = (long)gx * ((tk + BM - 1) / BM + std::min<long>(E, tk));               \
+    MM_CHECK_ARG(blocks < (1L << 30), "mm_moe_grouped_gemm: T*k=%ld too large", tk);           \
+    if (g % PF2_BK == 0)                                                                       \
+      hipLaunchKernelGGL((k_moe_prefill<WM, WN, RB, true>), dim3((unsigned)blocks),            \
+                         dim3(WM * WN * 64), 0, (hipStream_t)stream, (const f16*)X, sorted_idx, \
+                         offsets, gather, k, B, (const f16*)S, E, K, N, g, act, gx, (f16*)Y);  \
+    else                                                                                       \
+      hipLaunchKernelGGL((k_moe_prefill<WM, WN, RB, false>), dim3((unsigned)blocks),           \
+                         dim3(WM * WN * 64), 0, (hipStream_t)stream, (const f16*)X, sorted_idx, \
+                         offsets, gather, k, B, (const f16*)S, E, K, N, g, act, gx, (f16*)Y);  \
+  } while (0)
+    switch (cfg) {
+      case 0: MM_LAUNCH_MOE_PF(2, 4, 2); break;    // 128 x 256, 8 waves
+      case 1: MM_LAUNCH_MOE_PF(1, 4, 2); break;    // 64 x 256, 4 waves
+      case 2: MM_LAUNCH_MOE_PF(1, 8, 2); break;    // 64 x 512, 8 waves
+      case 3: MM_LAUNCH_MOE_PF(1, 4, 3); break;    // 96 x 256, 4 waves
+      default: MM_LAUNCH_MOE_PF(2, 4, 4); break;   // 256 x 256, 8 waves
+    }
+#undef MM_LAUNCH_MOE_PF
+    MM_CHECK_LAUNCH("mm_moe_grouped_gemm(prefill)");
+    return 0;
+  }
   const int tiles = act ? mm_cdiv(nout, SK_COLS) : mm_cdiv(N, 2 * SK_COLS);
   dim3 grid(tiles, 1, E);
   // Blocks the launch can keep busy: column tiles x experts that can hold a

@@ -56,7 +56,8 @@ def test_moe_expert_gemm_vs_oracle(rng):
 
 
 @pytest.mark.parametrize("E,T,k,H,I", [(8, 16, 2, 256, 128), (16, 40, 4, 512, 256),
-                                       (128, 32, 8, 2048, 768)])
+                                       (128, 32, 8, 2048, 768), (8, 256, 2, 256, 128),
+                                       (16, 200, 4, 512, 384), (16, 100, 4, 256, 128)])
 def test_moe_mlp_vs_oracle(rng, E, T, k, H, I):
     import mmfp4
     g = 128
@@ -68,6 +69,48 @@ def test_moe_mlp_vs_oracle(rng, E, T, k, H, I):
     announce(f"moe mlp E={E} T={T} k={k} H={H} I={I}")
     out = mmfp4.moe_mlp_fp4(to_dev(x), to_dev(GU), to_dev(GS), to_dev(DP), to_dev(DS),
                             to_dev(ids), to_dev(probs), g)
+    assert max_abs_rel(to_np(out), ref) <= TOL
+
+
+@pytest.mark.parametrize("g", [32, 64, 128])
+def test_moe_mlp_prefill_skewed(rng, g):
+    """MFMA tile path with ragged groups: expert 0 takes 300 of 400 tokens
+    (two full 128-row tiles and a partial one), expert 5 none, the rest a few
+    dozen; group sizes below, at and above the 64-k chunk."""
+    import mmfp4
+    E, T, k, H, I = 6, 400, 2, 256, 128
+    GU, GS = _experts(rng, E, H, 2 * I, g)
+    DP, DS = _experts(rng, E, I, H, g)
+    x = rng.normal(0, 1, (T, H)).astype(np.float16)
+    ids = np.zeros((T, k), np.int32)
+    ids[:, 0] = np.where(np.arange(T) < 300, 0, rng.integers(1, 5, T))
+    ids[:, 1] = (ids[:, 0] + rng.integers(1, 4, T)) % 5
+    ids[:, 1] = np.where(ids[:, 1] == ids[:, 0], 4, ids[:, 1])
+    assert (ids[:, 0] != ids[:, 1]).all() and not (ids == 5).any()
+    probs = rng.uniform(0.1, 1.0, (T, k)).astype(np.float32)
+    probs /= probs.sum(1, keepdims=True)
+    ref = omoe.moe_forward_ref(x, GU, GS, DP, DS, ids, probs, g)
+    announce(f"moe mlp prefill skewed g={g}")
+    out = mmfp4.moe_mlp_fp4(to_dev(x), to_dev(GU), to_dev(GS), to_dev(DP), to_dev(DS),
+                            to_dev(ids), to_dev(probs), g)
+    assert max_abs_rel(to_np(out), ref) <= TOL
+
+
+def test_moe_expert_gemm_prefill_vs_oracle(rng):
+    """moe_expert_gemm_fp4 with prefill-sized groups (gathered rows, no
+    activation) against the per-token fp32 brute force."""
+    import mmfp4
+    E, T, k, K, N, g = 4, 200, 2, 256, 200, 128
+    P, S = _experts(rng, E, K, N, g)
+    x = rng.normal(0, 1, (T, K)).astype(np.float16)
+    ids, probs = omoe.router_topk(rng.normal(0, 1, (T, E)), k)
+    W = [ofp4.dequant_fp4_f32(P[e], S[e], g) for e in range(E)]
+    ref = np.zeros((T, N), np.float32)
+    for t in range(T):
+        for j in range(k):
+            ref[t] += probs[t, j] * (x[t].astype(np.float32) @ W[ids[t, j]])
+    announce("moe_expert_gemm_fp4 prefill")
+    out = mmfp4.moe_expert_gemm_fp4(to_dev(x), to_dev(P), to_dev(S), to_dev(ids), to_dev(probs), g)
     assert max_abs_rel(to_np(out), ref) <= TOL
 
 
