@@ -90,6 +90,12 @@ int mm_u4_gemm(const uint16_t* A, const uint32_t* B, const uint16_t* scales,
 int mm_moe_sort(const int32_t* expert_ids, int T, int k, int E, int32_t* offsets,
                 int32_t* sorted_idx, int32_t* inverse, void* stream);
 
+/* mm_moe_sort for int64 expert ids (what torch.topk returns), so callers
+ * need no conversion launch.  Same outputs and errors; replaces the same
+ * reference functions. */
+int mm_moe_sort_i64(const int64_t* expert_ids, int T, int k, int E, int32_t* offsets,
+                    int32_t* sorted_idx, int32_t* inverse, void* stream);
+
 /* Grouped expert GEMM over expert-sorted rows.  For expert e, rows
  * r in [offsets[e], offsets[e+1]) compute Y[r] = X[row(r)] . dequant(B[e], S[e]),
  * where row(r) = sorted_idx[r] / k when gather != 0 (rows of X are tokens)

@@ -104,4 +104,4 @@ void mm_set_error(const char* fmt, ...);
     }                                                                     \
   } while (0)
 
-static inline int mm_cdiv(int a, int b) { return (a + b - 1) / b; }
+__host__ __device__ static inline int mm_cdiv(int a, int b) { return (a + b - 1) / b; }

@@ -393,6 +393,9 @@ k_splitk_reduce(const float* __restrict__ part, int ks, int M, int N, f16* __res
 #ifndef MM_SK_KS2
 #define MM_SK_KS2 4         // max K split for 16 < M <= 32 (bounds partial traffic)
 #endif
+#ifndef MM_SK_NOSPLIT_TILES
+#define MM_SK_NOSPLIT_TILES 200   // column tiles from which the K range is not split
+#endif
 #ifndef MM_SK_MAXBLOCKS
 #define MM_SK_MAXBLOCKS 2048
 #endif
@@ -421,6 +424,11 @@ SkinnyPlan plan_skinny(int M, int N, int K) {
   // partial-sum traffic (ksplit * M * N * 4 bytes each way).
   int ks = blocks_k;
   if ((long)ks * p.ntiles > MM_SK_MAXBLOCKS) ks = mm_cdiv(MM_SK_MAXBLOCKS, p.ntiles);
+  // With this many column tiles the grid already spreads over the CUs: a K
+  // split would only add the hand-off and a second round of blocks (two
+  // 8-wave blocks are resident per CU).  Measured on MI355X at M=1:
+  // 4096x28672 16.8 -> 13.3 us, 4096x14336 10.0 -> 8.3 us.
+  if (p.ntiles >= MM_SK_NOSPLIT_TILES) ks = 1;
   if (M > 16 && ks > MM_SK_KS2) ks = MM_SK_KS2;
   if (ks < 1) ks = 1;
   p.nrounds = mm_cdiv(blocks_k, ks);

@@ -25,79 +25,130 @@ using namespace mmpf;
 constexpr int SORT_THREADS = 1024;
 constexpr int MOE_MAX_EXPERTS = SORT_THREADS;   // the sort holds one expert per thread
 constexpr int SORT_WAVES = SORT_THREADS / 64;
+constexpr int SORT_KC = 8;          // 64-key chunks fetched together per wave
 
-// One block.  Dynamic LDS: cursor[E] + wcnt[SORT_WAVES][E] ints.
+// Stable counting sort in one block.  Wave w owns the w-th contiguous
+// segment of the flat assignments (whole 64-element chunks), so segment order
+// is index order.  Within a chunk, the lanes holding the same expert are found
+// with one ballot per key bit (log2(E) ballots, independent of how many
+// distinct experts the chunk holds); the lowest such lane is the group's
+// leader.  Pass 1 counts per (wave, expert); a scan turns the counts into
+// expert offsets and each wave's first position per expert; pass 2 places
+// every assignment at its wave's running position plus its rank among the
+// equal lanes below it.  Dynamic LDS: wpos[SORT_WAVES][E] ints.
+template <typename IdT>
 __global__ void __launch_bounds__(SORT_THREADS)
-k_moe_sort(const int32_t* __restrict__ ids, int n, int E, int32_t* __restrict__ offsets,
+k_moe_sort(const IdT* __restrict__ ids, int n, int E, int32_t* __restrict__ offsets,
            int32_t* __restrict__ sorted_idx, int32_t* __restrict__ inverse) {
-  extern __shared__ int lds[];
-  int* cursor = lds;            // [E]
-  int* wcnt = lds + E;          // [SORT_WAVES][E]
-  __shared__ int scan[SORT_THREADS];
+  extern __shared__ int wpos[];
+  __shared__ int wsum[SORT_WAVES];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nbits = E > 1 ? 32 - __clz(E - 1) : 0;
+  const int per = mm_cdiv(mm_cdiv(n, 64), SORT_WAVES) * 64;
+  const int seg0 = min(n, wave * per), seg1 = min(n, seg0 + per);
+  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  int* mine = wpos + wave * E;
 
-  for (int e = tid; e < E; e += SORT_THREADS) cursor[e] = 0;
+  for (int x = tid; x < SORT_WAVES * E; x += SORT_THREADS) wpos[x] = 0;
   __syncthreads();
-  for (int i = tid; i < n; i += SORT_THREADS) {
-    const int e = ids[i];
-    if (e >= 0 && e < E) atomicAdd(&cursor[e], 1);
+
+  // Keys past the segment read a clamped index (the load is unconditional, so
+  // the SORT_KC loads of a batch stay in flight together) and become -1.
+  auto key_at = [&](int i) {
+    const long long v = (long long)ids[min(i, n - 1)];
+    return (i < seg1 && v >= 0 && v < E) ? (int)v : -1;
+  };
+  auto match = [&](int key) {
+    const bool valid = key >= 0;
+    uint64_t m = __ballot(valid);
+    for (int bit = 0; bit < nbits; ++bit) {
+      const bool on = valid && ((key >> bit) & 1);
+      const uint64_t bb = __ballot(on);
+      m &= on ? bb : ~bb;
+    }
+    return valid ? m : 0ull;
+  };
+
+  // Keys are fetched SORT_KC chunks at a time so their loads overlap.  When
+  // the wave's segment is one such batch (n <= SORT_WAVES*64*SORT_KC), its
+  // keys, in-group ranks and group sizes stay in registers for pass 2.
+  const bool single = seg1 - seg0 <= 64 * SORT_KC;
+  int skey[SORT_KC], srank[SORT_KC], sgrp[SORT_KC];
+#pragma unroll
+  for (int c = 0; c < SORT_KC; ++c) skey[c] = -1, srank[c] = 0, sgrp[c] = 0;   // empty segment
+  for (int s0 = seg0; s0 < seg1; s0 += 64 * SORT_KC) {       // pass 1: counts
+#pragma unroll
+    for (int c = 0; c < SORT_KC; ++c) skey[c] = key_at(s0 + 64 * c + lane);
+#pragma unroll
+    for (int c = 0; c < SORT_KC; ++c) {
+      const int e = skey[c];
+      const uint64_t same = match(e);
+      srank[c] = __popcll(same & below);
+      sgrp[c] = (e >= 0 && srank[c] == 0) ? __popcll(same) : 0;   // set on the group's leader
+      if (sgrp[c]) mine[e] += sgrp[c];
+    }
   }
   __syncthreads();
-  // Exclusive scan of the per-expert counts (E <= SORT_THREADS).
-  const int mine = tid < E ? cursor[tid] : 0;
-  scan[tid] = mine;
-  __syncthreads();
-  for (int d = 1; d < SORT_THREADS; d <<= 1) {
-    const int v = tid >= d ? scan[tid - d] : 0;
-    __syncthreads();
-    scan[tid] += v;
-    __syncthreads();
+
+  // Expert totals -> exclusive offsets (wave scans, then a scan of the wave
+  // sums), and each wave's first position per expert.
+  int tot = 0;
+  if (tid < E)
+    for (int w = 0; w < SORT_WAVES; ++w) tot += wpos[w * E + tid];
+  int incl = tot;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int o = __shfl_up(incl, d);
+    if (lane >= d) incl += o;
   }
+  if (lane == 63) wsum[wave] = incl;
+  __syncthreads();
+  int wbase = 0;
+  for (int w = 0; w < wave; ++w) wbase += wsum[w];
   if (tid < E) {
-    const int excl = scan[tid] - mine;
-    cursor[tid] = excl;
-    offsets[tid] = excl;
+    int run = wbase + incl - tot;
+    offsets[tid] = run;
+    for (int w = 0; w < SORT_WAVES; ++w) {
+      const int c = wpos[w * E + tid];
+      wpos[w * E + tid] = run;
+      run += c;
+    }
   }
-  if (tid == 0) offsets[E] = scan[SORT_THREADS - 1];
+  if (tid == SORT_THREADS - 1) offsets[E] = wbase + incl;
   __syncthreads();
 
-  // Stable placement, 1024 assignments per pass.  Within a wave the rank of an
-  // assignment among equal experts comes from a ballot over the lanes below it;
-  // across waves from a per-expert prefix of the waves' counts.
-  for (int base = 0; base < n; base += SORT_THREADS) {
-    for (int x = tid; x < SORT_WAVES * E; x += SORT_THREADS) wcnt[x] = 0;
-    __syncthreads();
-    const int i = base + tid;
-    const int e = (i < n) ? ids[i] : -1;
-    const bool valid = e >= 0 && e < E;
-    uint64_t pending = __ballot(valid);
-    int rank = 0;
-    const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    while (pending) {
-      const int leader = __ffsll((unsigned long long)pending) - 1;
-      const int le = __shfl(e, leader);
-      const uint64_t same = __ballot(valid && e == le);
-      if (valid && e == le) rank = __popcll(same & below);
-      if (lane == leader) wcnt[wave * E + le] = __popcll(same);
-      pending &= ~same;
-    }
-    __syncthreads();
-    for (int x = tid; x < E; x += SORT_THREADS) {
-      int run = cursor[x];
-      for (int w = 0; w < SORT_WAVES; ++w) {
-        const int c = wcnt[w * E + x];
-        wcnt[w * E + x] = run;
-        run += c;
+  // Pass 2: placement.  Every lane reads its group's running position before
+  // the leader advances it past the group (LDS ops of a wave complete in
+  // order).
+  if (single) {
+#pragma unroll
+    for (int c = 0; c < SORT_KC; ++c) {
+      const int e = skey[c];
+      if (e >= 0) {
+        const int i = seg0 + 64 * c + lane;
+        const int pos = mine[e] + srank[c];
+        sorted_idx[pos] = i;
+        inverse[i] = pos;
       }
-      cursor[x] = run;
+      if (sgrp[c]) mine[e] += sgrp[c];
     }
-    __syncthreads();
-    if (valid) {
-      const int pos = wcnt[wave * E + e] + rank;
-      sorted_idx[pos] = i;
-      inverse[i] = pos;
+    return;
+  }
+  for (int s0 = seg0; s0 < seg1; s0 += 64 * SORT_KC) {
+#pragma unroll
+    for (int c = 0; c < SORT_KC; ++c) skey[c] = key_at(s0 + 64 * c + lane);
+#pragma unroll
+    for (int c = 0; c < SORT_KC; ++c) {
+      const int i = s0 + 64 * c + lane;
+      const int e = skey[c];
+      const uint64_t same = match(e);
+      if (e >= 0) {
+        const int pos = mine[e] + __popcll(same & below);
+        sorted_idx[pos] = i;
+        inverse[i] = pos;
+      }
+      if (e >= 0 && (same & below) == 0) mine[e] += __popcll(same);
     }
-    __syncthreads();
   }
 }
 
@@ -318,21 +369,34 @@ k_moe_combine(const f16* __restrict__ Y, const float* __restrict__ probs,
   }
 }
 
+template <typename IdT>
+int moe_sort(const char* who, const IdT* expert_ids, int T, int k, int E, int32_t* offsets,
+             int32_t* sorted_idx, int32_t* inverse, void* stream) {
+  MM_CHECK_ARG(T >= 0 && k > 0, "%s: bad T=%d k=%d", who, T, k);
+  MM_CHECK_ARG(E > 0 && E <= SORT_THREADS, "%s: num_experts=%d must be in [1, %d]", who, E,
+               SORT_THREADS);
+  MM_CHECK_ARG((long)T * k < (1L << 30), "%s: T*k too large", who);
+  const size_t lds = (size_t)SORT_WAVES * E * sizeof(int);
+  hipLaunchKernelGGL(k_moe_sort<IdT>, dim3(1), dim3(SORT_THREADS), lds, (hipStream_t)stream,
+                     expert_ids, T * k, E, offsets, sorted_idx, inverse);
+  MM_CHECK_LAUNCH(who);
+  return 0;
+}
+
 }  // namespace
 
 // ===========================================================================
 // C ABI
 // ===========================================================================
+
 extern "C" int mm_moe_sort(const int32_t* expert_ids, int T, int k, int E, int32_t* offsets,
                            int32_t* sorted_idx, int32_t* inverse, void* stream) {
-  MM_CHECK_ARG(T >= 0 && k > 0, "mm_moe_sort: bad T=%d k=%d", T, k);
-  MM_CHECK_ARG(E > 0 && E <= SORT_THREADS, "mm_moe_sort: num_experts=%d must be in [1, %d]", E,
-               SORT_THREADS);
-  const size_t lds = (size_t)(SORT_WAVES + 1) * E * sizeof(int);
-  hipLaunchKernelGGL(k_moe_sort, dim3(1), dim3(SORT_THREADS), lds, (hipStream_t)stream,
-                     expert_ids, T * k, E, offsets, sorted_idx, inverse);
-  MM_CHECK_LAUNCH("mm_moe_sort");
-  return 0;
+  return moe_sort("mm_moe_sort", expert_ids, T, k, E, offsets, sorted_idx, inverse, stream);
+}
+
+extern "C" int mm_moe_sort_i64(const int64_t* expert_ids, int T, int k, int E, int32_t* offsets,
+                               int32_t* sorted_idx, int32_t* inverse, void* stream) {
+  return moe_sort("mm_moe_sort_i64", expert_ids, T, k, E, offsets, sorted_idx, inverse, stream);
 }
 
 extern "C" int mm_moe_grouped_gemm(const uint16_t* X, const int32_t* sorted_idx,

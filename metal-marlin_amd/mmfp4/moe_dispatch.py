@@ -42,11 +42,14 @@ def _sort(expert_ids: torch.Tensor, num_experts: int):
     if expert_ids.dim() != 2:
         raise ValueError("expert_ids must be [batch, top_k]")
     T, k = expert_ids.shape
-    ids = expert_ids.to(torch.int32).contiguous()
+    if expert_ids.dtype == torch.int64:
+        ids, entry = expert_ids.contiguous(), "mm_moe_sort_i64"
+    else:
+        ids, entry = expert_ids.to(torch.int32).contiguous(), "mm_moe_sort"
     offsets = torch.empty(num_experts + 1, dtype=torch.int32, device=dev)
     sorted_idx = torch.empty(T * k, dtype=torch.int32, device=dev)
     inverse = torch.empty(T * k, dtype=torch.int32, device=dev)
-    _lib.call("mm_moe_sort", _lib.ptr(ids), T, k, num_experts, _lib.ptr(offsets),
+    _lib.call(entry, _lib.ptr(ids), T, k, num_experts, _lib.ptr(offsets),
               _lib.ptr(sorted_idx), _lib.ptr(inverse), _lib.stream_of(ids))
     return sorted_idx, offsets, inverse
 

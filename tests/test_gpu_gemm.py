@@ -154,10 +154,40 @@ def test_split_k_workspace_reuse_across_shapes():
     """Counters left at zero: interleaved shapes reproduce their first result."""
     import mmfp4
     probs = [_gpu_problem(M, K, N, 128, seed=M + K) for M, K, N in
-             [(1, 14336, 4096), (8, 4096, 6144), (32, 14336, 512), (3, 4096, 128)]]
+             [(1, 14336, 4096), (8, 4096, 6144), (32, 14336, 512), (3, 4096, 128),
+              (32, 4096, 28672), (16, 14336, 4096)]]
     announce("workspace reuse")
     first = [mmfp4.marlin_gemm_fp4(a, p, s, 128) for a, p, s, _ in probs]
     for _ in range(3):
         for (a, p, s, _), f in zip(probs, first):
             assert torch.equal(mmfp4.marlin_gemm_fp4(a, p, s, 128).view(torch.int16),
                                f.view(torch.int16))
+
+
+@pytest.mark.parametrize("M,K", [(1, 4096), (8, 14336), (32, 4096)])
+def test_split_k_large_and_nonfinite_partials(M, K):
+    """Split-K partials outside the fixed-point range (|p| >= 2^15), that
+    cancel across splits, and inf / NaN inputs: same finite values (to the
+    tolerance), same NaN and same signed-inf positions as the fp32 reference."""
+    import mmfp4
+    N, g = 256, 128
+    gen = torch.Generator(device="cuda").manual_seed(9)
+    packed = torch.randint(-2**31, 2**31 - 1, (K // 8, N), generator=gen, dtype=torch.int32,
+                           device="cuda")
+    scales = (torch.rand((K // g, N), generator=gen, device="cuda") + 0.5).half()
+    a = torch.randn((M, K), generator=gen, device="cuda").half()
+    a[0, 5] = 30000.0            # first split: |partial| >> 2^15 ...
+    a[0, K - 7] = -30000.0       # ... cancelled by the last split
+    if M > 1:
+        a[1, 100] = float("inf")
+        a[1, K - 100] = float("-inf")
+        a[M - 1, K // 2] = float("nan")
+    ref = (a.float() @ mmfp4.dequant_fp4(packed, scales, K, N, g).float()).half().float()
+    announce(f"split-K big/non-finite partials M={M} K={K}")
+    out = mmfp4.marlin_gemm_fp4(a, packed, scales, g).float()
+    assert torch.equal(torch.isnan(out), torch.isnan(ref))
+    assert torch.equal(torch.isposinf(out), torch.isposinf(ref))
+    assert torch.equal(torch.isneginf(out), torch.isneginf(ref))
+    fin = torch.isfinite(ref)
+    err = (out[fin] - ref[fin]).abs().max().item()
+    assert err <= TOL * ref[fin].abs().max().item()

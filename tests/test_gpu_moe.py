@@ -15,14 +15,16 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.mark.parametrize("T,k,E", [(3, 2, 3), (1, 1, 4), (32, 8, 128), (1024, 8, 128),
-                                   (37, 3, 1000), (2000, 2, 8)])
-def test_sort_exact(rng, T, k, E):
+                                   (37, 3, 1000), (2000, 2, 8), (70, 1, 1), (8192, 8, 1024),
+                                   (0, 4, 16)])
+@pytest.mark.parametrize("dtype", [np.int32, np.int64])
+def test_sort_exact(rng, T, k, E, dtype):
     import mmfp4
     ids = rng.integers(0, E, (T, k)).astype(np.int32)
     if E > 4:
         ids[ids == 1] = 0          # leave some experts empty
-    announce(f"moe sort T={T} k={k} E={E}")
-    s, off, inv = mmfp4.group_tokens_by_expert(to_dev(ids), E)
+    announce(f"moe sort T={T} k={k} E={E} {np.dtype(dtype).name}")
+    s, off, inv = mmfp4.group_tokens_by_expert(to_dev(ids.astype(dtype)), E)
     rs, roff, rinv = omoe.group_tokens_by_expert(ids, E)
     assert np.array_equal(to_np(s), rs)
     assert np.array_equal(to_np(off), roff)
