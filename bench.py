@@ -253,7 +253,7 @@ def pmc_probe(torch, mmfp4) -> int:
     """Dispatches whose hardware counters calibrate and measure HBM traffic:
     one copy of 512 MiB (known: 512 MiB read + 512 MiB written), then every
     Llama-layer GEMM at M=1 on 4 rotated weight copies x 5, then the two
-    M=2048 prefill GEMMs x 2."""
+    M=2048 prefill GEMMs x 2, then the MoE MLP at T=32 and T=1024 x 2."""
     src = torch.empty(512 << 20, dtype=torch.uint8, device="cuda").fill_(1)
     dst = torch.empty_like(src)
     torch.cuda.synchronize()
@@ -273,6 +273,22 @@ def pmc_probe(torch, mmfp4) -> int:
         a = torch.randn((2048, K), device="cuda").half()
         for _ in range(2):
             mmfp4.marlin_gemm_fp4(a, w[0], w[1], G)
+        torch.cuda.synchronize()
+    # MoE (config 5) at T=32 and T=1024, two calls each on one weight set.
+    E, H, I, k = MOE["E"], MOE["H"], MOE["I"], MOE["k"]
+    gen = torch.Generator(device="cuda").manual_seed(600)
+    gu_p = torch.randint(-2**31, 2**31 - 1, (E, H // 8, 2 * I), generator=gen, dtype=torch.int32,
+                         device="cuda")
+    gu_s = (torch.rand((E, H // G, 2 * I), generator=gen, device="cuda") * 0.01).half()
+    dn_p = torch.randint(-2**31, 2**31 - 1, (E, I // 8, H), generator=gen, dtype=torch.int32,
+                         device="cuda")
+    dn_s = (torch.rand((E, I // G, H), generator=gen, device="cuda") * 0.01).half()
+    for T in (32, 1024):
+        p, ids = torch.topk(torch.softmax(torch.randn((T, E), generator=gen, device="cuda"), -1),
+                            k, -1)
+        x = torch.randn((T, H), generator=gen, device="cuda").half()
+        for _ in range(2):
+            mmfp4.moe_mlp_fp4(x, gu_p, gu_s, dn_p, dn_s, ids, p / p.sum(-1, keepdim=True), G)
         torch.cuda.synchronize()
     print(json.dumps({"pmc_probe": "done"}))
     return 0
@@ -330,12 +346,12 @@ def main() -> int:
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic("k_skinny_llama3_layer_m1.md"),
                      "traffic_source": "profiles/k_skinny_llama3_layer_m1.md",
-                     "kernel": "k_skinny (M<=32 decode path)",
+                     "kernel": "k_skinny + k_strip (M<=16 decode path, 4 launches per layer)",
                      "launch_us_avg": round(layer["launch_us_avg"], 3)},
         "per_shape_m1": layer["per_shape"],
         "prefill_m2048": {"tflops": round(tflops, 1), "frac_fp16_peak": round(tflops /
                           FP16_PEAK_TFLOPS, 4), "ms_per_step": round(pre["ms_per_step"], 4),
-                          "per_shape": pre["per_shape"], "kernel": "k_prefill (MFMA 32x32x16)"},
+                          "per_shape": pre["per_shape"], "kernel": "k_prefill2 (MFMA 32x32x16, global->LDS pipeline)"},
     }
     out["config1_single_linear_m1"] = run_single_bench(torch, mmfp4, 1, 4096, 4096, 100)
     out["config5_moe_qwen3_30b_a3b"] = [run_moe_bench(torch, mmfp4, T, 20) for T in (32, 1024)]
