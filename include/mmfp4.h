@@ -79,6 +79,20 @@ int mm_u4_gemm(const uint16_t* A, const uint32_t* B, const uint16_t* scales,
                const uint16_t* zeros, uint16_t* C, int M, int N, int K, int group_size, void* ws,
                size_t ws_bytes, void* stream);
 
+/* Gate and up projections over two packed FP4 matrices (Marlin [K/8, N],
+ * scales [K/g, N]) in one launch, reading A once:
+ *   act = 1:  C[M, N]  = silu(A . dequant(Bg, Sg)) * (A . dequant(Bu, Su))
+ *             (SiLU on the fp32 sums);
+ *   act = 0:  C[M, 2N] = [A . dequant(Bg, Sg) | A . dequant(Bu, Su)].
+ * Replaces metal_marlin/kernels_core.py:4749-4774 (fused_gate_up_gemm,
+ * mmfp4_fused_gate_up) -> MetalKernels.fused_gate_up_gemm :4220-4267 and
+ * .mmfp4_fused_gate_up :4269-4408.  Workspace: mm_gemm_workspace_bytes(M, 2N, K).
+ * Requires K % 8 == 0, N % 8 == 0, group_size % 8 == 0, K % group_size == 0,
+ * K % 64 == 0 when M > 32; A, weights and scales 16-byte aligned, C 8-byte. */
+int mm_fp4_gate_up(const uint16_t* A, const uint32_t* Bg, const uint16_t* Sg, const uint32_t* Bu,
+                   const uint16_t* Su, uint16_t* C, int M, int N, int K, int group_size, int act,
+                   void* ws, size_t ws_bytes, void* stream);
+
 /* -------------------------------------------------------------------- MoE */
 
 /* Stable counting sort of the T*k (token, slot) assignments by expert.

@@ -30,20 +30,38 @@ using namespace mmpf;
 
 constexpr int SK_RED_BATCH = 8;   // partial-sum loads in flight per thread
 
-// Dense skinny kernel.  grid = (ceil(N / (NT*64)), ksplit).
-template <bool INT4, int MT, int NT, int SPW, int NW, int FL>
+// SiLU(gate) * up in fp32 (the gate/up sums are never rounded to fp16 first).
+MM_DEV float swiglu(float gate, float up) { return gate / (1.0f + __expf(-gate)) * up; }
+
+// Epilogue modes of the dense skinny kernel.
+//   SK_PLAIN : C[:, n] = A . W[:, n]                          (one matrix)
+//   SK_SWIGLU: C[:, n] = silu(A . Wg[:, n]) * (A . Wu[:, n])   (gate, up; C is [M, N])
+//   SK_PAIR  : C[:, n] = A . Wg[:, n], C[:, N + n] = A . Wu[:, n]   (C is [M, 2N])
+enum { SK_PLAIN = 0, SK_SWIGLU = 1, SK_PAIR = 2 };
+
+// Dense skinny kernel.  grid = (column tiles, ksplit).  SK_PLAIN: a block
+// covers NT adjacent 64-column tiles of B.  SK_SWIGLU / SK_PAIR (NT = 2):
+// tile 0 is columns [n0, n0+64) of (B, S, Z) and tile 1 the same columns of
+// (B2, S2, Z2).  Split-K partials are [ksplit][M][PW] fp32 with PW = N, or
+// 2N for the pair modes (gate at n, up at N + n).
+template <bool INT4, int MT, int NT, int SPW, int NW, int FL, int ACT>
 __global__ void __launch_bounds__(NW * 64)
 k_skinny(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
-         const f16* __restrict__ S, const f16* __restrict__ Z, f16* __restrict__ C, int ldc,
+         const f16* __restrict__ S, const f16* __restrict__ Z, const uint32_t* __restrict__ B2,
+         const f16* __restrict__ S2, const f16* __restrict__ Z2, f16* __restrict__ C, int ldc,
          int M, int N, int K, int g, int nrounds, float* __restrict__ part,
          uint32_t* __restrict__ counters) {
+  static_assert(ACT == SK_PLAIN || NT == 2, "pair modes use one tile of each matrix");
   constexpr int RED = (NW > 1 ? NW - 1 : 1) * MT * NT * 16 * 64;
   __shared__ float red[RED];
   __shared__ uint32_t s_last;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int c = lane & 15, q = lane >> 4;
-  const int n0 = blockIdx.x * NT * SK_COLS;
+  const int n0 = blockIdx.x * (ACT == SK_PLAIN ? NT : 1) * SK_COLS;
   const int ksplit = gridDim.y;
+  const int PW = ACT == SK_PLAIN ? N : 2 * N;
+  // Column of tile t (lane group c) in the partial-sum row, and in C.
+  auto pcol = [&](int t) { return ACT == SK_PLAIN ? n0 + t * SK_COLS + 4 * c : t * N + n0 + 4 * c; };
   // Steps owned by this block: NW*SPW*nrounds consecutive 32-k steps; waves
   // take interleaved SPW-step slabs so each round reads adjacent word rows.
   const int blk_st0 = blockIdx.y * NW * SPW * nrounds;
@@ -55,25 +73,42 @@ k_skinny(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc[mt][t][j] = f32x4{0, 0, 0, 0};
 
-  skinny_wave<INT4, MT, NT, SPW, FL>(A, lda, nullptr, 1, M, B, S, Z, N, K, g, n0, SK_COLS,
-                                 blk_st0 + wave * SPW, nrounds, NW * SPW, acc);
+  SkTile tl[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+    tl[t] = ACT == SK_PLAIN ? SkTile{B, S, Z, n0 + t * SK_COLS}
+                            : (t == 0 ? SkTile{B, S, Z, n0} : SkTile{B2, S2, Z2, n0});
+  skinny_wave<INT4, MT, NT, SPW, FL>(A, lda, nullptr, 1, M, tl, N, K, g, blk_st0 + wave * SPW,
+                                     nrounds, NW * SPW, acc);
   skinny_block_reduce<MT, NT, NW>(red, acc);
 
-  // Lane (c, q) of wave 0 holds rows 16*mt + 4*q + rr, columns n0 + 64*t + 4*c + j.
+  // Lane (c, q) of wave 0 holds rows 16*mt + 4*q + rr, columns 4*c + j of
+  // each tile.
   if (ksplit == 1) {
     if (wave != 0) return;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        const int col = n0 + t * SK_COLS + 4 * c;
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          const int row = mt * 16 + 4 * q + rr;
-          if (row < M && col < N)
+      for (int rr = 0; rr < 4; ++rr) {
+        const int row = mt * 16 + 4 * q + rr;
+        if (row >= M) continue;
+        if constexpr (ACT == SK_SWIGLU) {
+          const int col = n0 + 4 * c;
+          if (col < N)
             *(f16x4*)(C + (size_t)row * ldc + col) =
-                f16x4{(f16)acc[mt][t][0][rr], (f16)acc[mt][t][1][rr], (f16)acc[mt][t][2][rr],
-                      (f16)acc[mt][t][3][rr]};
+                f16x4{(f16)swiglu(acc[mt][0][0][rr], acc[mt][1][0][rr]),
+                      (f16)swiglu(acc[mt][0][1][rr], acc[mt][1][1][rr]),
+                      (f16)swiglu(acc[mt][0][2][rr], acc[mt][1][2][rr]),
+                      (f16)swiglu(acc[mt][0][3][rr], acc[mt][1][3][rr])};
+        } else {
+#pragma unroll
+          for (int t = 0; t < NT; ++t) {
+            const int col = ACT == SK_PLAIN ? n0 + t * SK_COLS + 4 * c : n0 + 4 * c;
+            if (col < N)
+              *(f16x4*)(C + (size_t)row * ldc + pcol(t)) =
+                  f16x4{(f16)acc[mt][t][0][rr], (f16)acc[mt][t][1][rr], (f16)acc[mt][t][2][rr],
+                        (f16)acc[mt][t][3][rr]};
+          }
         }
       }
     return;
@@ -88,12 +123,12 @@ k_skinny(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
-        const int col = n0 + t * SK_COLS + 4 * c;
+        const int col = ACT == SK_PLAIN ? n0 + t * SK_COLS + 4 * c : n0 + 4 * c;
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
           const int row = mt * 16 + 4 * q + rr;
           if (row < M && col < N) {
-            float* dst = part + ((size_t)blockIdx.y * M + row) * N + col;
+            float* dst = part + ((size_t)blockIdx.y * M + row) * PW + pcol(t);
 #pragma unroll
             for (int j = 0; j < 4; ++j)
               __hip_atomic_store(dst + j, acc[mt][t][j][rr], __ATOMIC_RELAXED,
@@ -116,36 +151,48 @@ k_skinny(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
   if (!s_last) return;
   // One thread per (row, 4-column) item sums the splits in order; the loads of
   // SK_RED_BATCH splits are issued together so the chain is ksplit/8 trips.
-  constexpr int COLS = NT * SK_COLS;
-  const int nitems = min(M, MT * 16) * (COLS / 4);
-  for (int e = threadIdx.x; e < nitems; e += NW * 64) {
-    const int row = e / (COLS / 4), col = n0 + 4 * (e % (COLS / 4));
-    if (col >= N) continue;
-    float v[4] = {0, 0, 0, 0};
+  // SK_SWIGLU items carry the gate and the up columns of one 4-column group.
+  auto sum_splits = [&](int row, int pc) {
+    f32x4 v = {0, 0, 0, 0};
     for (int y0 = 0; y0 < ksplit; y0 += SK_RED_BATCH) {
-      float ld[SK_RED_BATCH][4];
+      f32x4 ld[SK_RED_BATCH];
 #pragma unroll
       for (int i = 0; i < SK_RED_BATCH; ++i) {
         const int y = min(y0 + i, ksplit - 1);
-        const float* src = part + ((size_t)y * M + row) * N + col;
+        const float* src = part + ((size_t)y * M + row) * PW + pc;
 #pragma unroll
         for (int j = 0; j < 4; ++j)
           ld[i][j] = __hip_atomic_load(src + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
 #pragma unroll
       for (int i = 0; i < SK_RED_BATCH; ++i)
-        if (y0 + i < ksplit)
-#pragma unroll
-          for (int j = 0; j < 4; ++j) v[j] += ld[i][j];
+        if (y0 + i < ksplit) v += ld[i];
     }
-    *(f16x4*)(C + (size_t)row * ldc + col) = f16x4{(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
+    return v;
+  };
+  constexpr int GROUPS = (ACT == SK_SWIGLU ? 1 : NT) * SK_COLS / 4;   // 4-column items per row
+  const int nitems = min(M, MT * 16) * GROUPS;
+  for (int e = threadIdx.x; e < nitems; e += NW * 64) {
+    const int row = e / GROUPS, gi = e % GROUPS;
+    if constexpr (ACT == SK_SWIGLU) {
+      const int col = n0 + 4 * gi;
+      if (col >= N) continue;
+      const f32x4 gt = sum_splits(row, col), up = sum_splits(row, N + col);
+      *(f16x4*)(C + (size_t)row * ldc + col) =
+          f16x4{(f16)swiglu(gt[0], up[0]), (f16)swiglu(gt[1], up[1]),
+                (f16)swiglu(gt[2], up[2]), (f16)swiglu(gt[3], up[3])};
+    } else {
+      const int t = gi / (SK_COLS / 4);
+      const int col = (ACT == SK_PLAIN ? n0 + t * SK_COLS : n0) + 4 * (gi % (SK_COLS / 4));
+      if (col >= N) continue;
+      const int pc = ACT == SK_PLAIN ? col : t * N + col;
+      const f32x4 v = sum_splits(row, pc);
+      *(f16x4*)(C + (size_t)row * ldc + pc) = f16x4{(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
+    }
   }
   if (threadIdx.x == 0)
     __hip_atomic_store(&counters[blockIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-
-
-
 
 // Column-strip kernel (M <= 16, group size a multiple of 32): one block per
 // NS*16 columns over the whole K; no split-K and no workspace.
@@ -312,43 +359,77 @@ struct DenseSrc {
   const f16* Z;
   int ld;
   MM_DEV const f16* arow(int r) const { return A + (size_t)min(m0 + r, M - 1) * lda; }
-  MM_DEV int col(int P, int w) const { return min(n0 + P, N - w); }
+  MM_DEV const uint32_t* bcol(int P, int w) const { return B + min(n0 + P, N - w); }
+  MM_DEV const f16* scol(int P, int w) const { return S + min(n0 + P, N - w); }
+  MM_DEV const f16* zcol(int P, int w) const { return Z + min(n0 + P, N - w); }
 };
 
-template <bool INT4, int WM, int WN, int RB, int CW, bool G64>
+// Gate/up pair: (B, S, Z) gate and (B2, S2, Z2) up matrices, both [.., N];
+// n0 is the block's first output column.
+struct PairSrc {
+  const f16* A;
+  int lda, M, m0, N, n0;
+  const uint32_t *B, *B2;
+  const f16 *S, *S2, *Z, *Z2;
+  int ld;
+  MM_DEV const f16* arow(int r) const { return A + (size_t)min(m0 + r, M - 1) * lda; }
+  MM_DEV const uint32_t* bcol(int P, int w) const {
+    return (pair_is_up(P) ? B2 : B) + pair_out_col(n0, P, w, N);
+  }
+  MM_DEV const f16* scol(int P, int w) const {
+    return (pair_is_up(P) ? S2 : S) + pair_out_col(n0, P, w, N);
+  }
+  MM_DEV const f16* zcol(int P, int w) const {
+    return (pair_is_up(P) ? Z2 : Z) + pair_out_col(n0, P, w, N);
+  }
+};
+
+template <bool INT4, int WM, int WN, int RB, int CW, bool G64, int ACT>
 __global__ void __launch_bounds__(WM * WN * 64)
 k_prefill2(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
-           const f16* __restrict__ S, const f16* __restrict__ Z, f16* __restrict__ C, int ldc,
+           const f16* __restrict__ S, const f16* __restrict__ Z, const uint32_t* __restrict__ B2,
+           const f16* __restrict__ S2, const f16* __restrict__ Z2, f16* __restrict__ C, int ldc,
            int M, int N, int K, int g, float* __restrict__ part) {
-  // Wave tile: (32*RB) rows x (32*CW) columns; lane l32 owns CW adjacent
-  // columns (CW packed words of one word row feed CW column tiles).
-  // Requires K % 64 == 0 and N % 8 == 0 (checked by the host).
+  // Wave tile: (32*RB) rows x (32*CW) LDS columns.  SK_PLAIN: lane l32 owns
+  // CW adjacent columns (CW packed words of one word row feed CW column
+  // tiles).  Pair modes (CW = 2, tile-major): column tile 0 is 32 gate
+  // columns and tile 1 the same 32 up columns, so a block covers BN/2 output
+  // columns.  Requires K % 64 == 0 and N % 8 == 0 (checked by the host).
+  static_assert(ACT == SK_PLAIN || CW == 2, "pair modes pair two column tiles");
   using Sh = Pf2Shape<INT4, WM, WN, RB, CW>;
   __shared__ __attribute__((aligned(16))) char smem[Sh::LDS_BYTES];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / WN, wn = wave % WN;
   const int l32 = lane & 31, h = lane >> 5;
-  const int m0 = blockIdx.y * Sh::BM, n0 = blockIdx.x * Sh::BN;
+  const int m0 = blockIdx.y * Sh::BM;
+  const int n0 = blockIdx.x * (ACT == SK_PLAIN ? Sh::BN : Sh::BN / 2);
   // K split: blockIdx.z owns chunks [c_beg, c_end); with gridDim.z > 1 the
-  // tile is written as an fp32 partial to part[z][M][N] instead of C.
+  // tile is written as an fp32 partial to part[z][M][PW] instead of C.
   const int nch_all = K / PF2_BK;
   const int cps = (nch_all + gridDim.z - 1) / gridDim.z;
   const int c_beg = blockIdx.z * cps;
   const int c_end = min(nch_all, c_beg + cps);
-  const DenseSrc src{A, lda, M, m0, N, n0, B, S, Z, N};
   f32x16 acc[RB][CW];
-  pf2_mainloop<INT4, WM, WN, RB, CW, G64, false>(src, K, g, c_beg, c_end, RB, smem, acc);
+  if constexpr (ACT == SK_PLAIN) {
+    const DenseSrc src{A, lda, M, m0, N, n0, B, S, Z, N};
+    pf2_mainloop<INT4, WM, WN, RB, CW, G64, false>(src, K, g, c_beg, c_end, RB, smem, acc);
+  } else {
+    const PairSrc src{A, lda, M, m0, N, n0, B, B2, S, S2, Z, Z2, N};
+    pf2_mainloop<INT4, WM, WN, RB, CW, G64, true>(src, K, g, c_beg, c_end, RB, smem, acc);
+  }
 
-  const int ncol = n0 + wn * 32 * CW + CW * l32;
-  if (ncol >= N) return;
   typedef f16 svec __attribute__((ext_vector_type(CW)));
   typedef float fvec __attribute__((ext_vector_type(CW)));
+  const int PW = ACT == SK_PLAIN ? N : 2 * N;
+  const int ncol = ACT == SK_PLAIN ? n0 + wn * 32 * CW + CW * l32 : n0 + wn * 32 + l32;
+  if (ncol >= N) return;
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
       const int row = m0 + wm * 32 * RB + rb * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-      if (row < M) {
+      if (row >= M) continue;
+      if constexpr (ACT == SK_PLAIN) {
         if (gridDim.z == 1) {
           svec o;
 #pragma unroll
@@ -358,23 +439,44 @@ k_prefill2(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
           fvec o;
 #pragma unroll
           for (int j = 0; j < CW; ++j) o[j] = acc[rb][j][v];
-          *(fvec*)(part + ((size_t)blockIdx.z * M + row) * N + ncol) = o;
+          *(fvec*)(part + ((size_t)blockIdx.z * M + row) * PW + ncol) = o;
         }
+      } else if (gridDim.z > 1) {
+        float* prow = part + ((size_t)blockIdx.z * M + row) * PW;
+        prow[ncol] = acc[rb][0][v];
+        prow[N + ncol] = acc[rb][1][v];
+      } else if constexpr (ACT == SK_SWIGLU) {
+        C[(size_t)row * ldc + ncol] = (f16)swiglu(acc[rb][0][v], acc[rb][1][v]);
+      } else {
+        C[(size_t)row * ldc + ncol] = (f16)acc[rb][0][v];
+        C[(size_t)row * ldc + N + ncol] = (f16)acc[rb][1][v];
       }
     }
   }
 }
 
 // Sum the K-split partials of the prefill kernel in split order -> fp16 C.
+// Partials are [ks][M][PW]; PW = N, or 2N for the pair modes (gate at n, up
+// at N + n).  SK_SWIGLU writes silu(gate) * up to C [M, N]; the others copy
+// the PW sums to C.
+template <int ACT>
 __global__ void __launch_bounds__(256)
 k_splitk_reduce(const float* __restrict__ part, int ks, int M, int N, f16* __restrict__ C,
                 int ldc) {
+  const int PW = ACT == SK_PLAIN ? N : 2 * N;
+  const int OW = ACT == SK_SWIGLU ? N : PW;                       // output columns
   const size_t i4 = (size_t)blockIdx.x * 256 + threadIdx.x;     // 4-column item
-  const size_t items = (size_t)M * (N / 4);
+  const size_t items = (size_t)M * (OW / 4);
   if (i4 >= items) return;
-  const int row = (int)(i4 / (N / 4)), col = 4 * (int)(i4 % (N / 4));
-  f32x4 v = {0, 0, 0, 0};
-  for (int z = 0; z < ks; ++z) v += *(const f32x4*)(part + ((size_t)z * M + row) * N + col);
+  const int row = (int)(i4 / (OW / 4)), col = 4 * (int)(i4 % (OW / 4));
+  f32x4 v = {0, 0, 0, 0}, u = {0, 0, 0, 0};
+  for (int z = 0; z < ks; ++z) {
+    const float* prow = part + ((size_t)z * M + row) * PW;
+    v += *(const f32x4*)(prow + col);
+    if constexpr (ACT == SK_SWIGLU) u += *(const f32x4*)(prow + N + col);
+  }
+  if constexpr (ACT == SK_SWIGLU)
+    v = f32x4{swiglu(v[0], u[0]), swiglu(v[1], u[1]), swiglu(v[2], u[2]), swiglu(v[3], u[3])};
   *(f16x4*)(C + (size_t)row * ldc + col) = f16x4{(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
 }
 
@@ -447,28 +549,34 @@ size_t skinny_ws_bytes(int M, int N, int K) {
   return SK_COUNTER_BYTES + (size_t)p.ksplit * M * N * sizeof(float);
 }
 
-template <bool INT4, int MT>
-int launch_skinny(const f16* A, int lda, const uint32_t* B, const f16* S, const f16* Z, f16* C,
-                  int ldc, int M, int N, int K, int g, void* ws, size_t ws_bytes,
-                  hipStream_t st) {
-  const SkinnyPlan p = plan_skinny(M, N, K);
-  constexpr int NT = sk_nt<MT>();
-  MM_CHECK_ARG(p.ntiles <= SK_MAX_TILES, "gemm: N=%d exceeds the supported %d columns", N,
-               SK_MAX_TILES * NT * SK_COLS);
+// ACT = SK_PLAIN: C = A . B.  Pair modes: B/S/Z is the gate matrix and
+// B2/S2/Z2 the up matrix, both [.., N]; the split and workspace are those of
+// the unfused [K, 2N] product (plan_skinny(M, 2N, K)).
+template <bool INT4, int MT, int ACT>
+int launch_skinny(const f16* A, int lda, const uint32_t* B, const f16* S, const f16* Z,
+                  const uint32_t* B2, const f16* S2, const f16* Z2, f16* C, int ldc, int M,
+                  int N, int K, int g, void* ws, size_t ws_bytes, hipStream_t st) {
+  const int PW = ACT == SK_PLAIN ? N : 2 * N;
+  const SkinnyPlan p = plan_skinny(M, PW, K);
+  constexpr int NT = ACT == SK_PLAIN ? sk_nt<MT>() : 2;
+  const int gx = ACT == SK_PLAIN ? p.ntiles : mm_cdiv(N, SK_COLS);
+  MM_CHECK_ARG(gx <= SK_MAX_TILES, "gemm: N=%d exceeds the supported %d columns", N,
+               SK_MAX_TILES * SK_COLS);
   uint32_t* counters = (uint32_t*)ws;
   float* part = nullptr;
   if (p.ksplit > 1) {
-    const size_t need = skinny_ws_bytes(M, N, K);
+    const size_t need = skinny_ws_bytes(M, PW, K);
     MM_CHECK_ARG(ws != nullptr && ws_bytes >= need,
                  "gemm: workspace of %zu bytes is smaller than the %zu required", ws_bytes, need);
     part = (float*)((char*)ws + SK_COUNTER_BYTES);
   }
-  dim3 grid(p.ntiles, p.ksplit);
+  dim3 grid(gx, p.ksplit);
   constexpr int SPW = sk_spw<MT>();
   const int fl = flush_steps(g, SPW);
 #define MM_LAUNCH_SK(FLV)                                                                   \
-  hipLaunchKernelGGL((k_skinny<INT4, MT, NT, SPW, SK_NW, FLV>), grid, dim3(SK_NW * 64), 0, st, \
-                     A, lda, B, S, Z, C, ldc, M, N, K, g, p.nrounds, part, counters)
+  hipLaunchKernelGGL((k_skinny<INT4, MT, NT, SPW, SK_NW, FLV, ACT>), grid, dim3(SK_NW * 64), 0, \
+                     st, A, lda, B, S, Z, B2, S2, Z2, C, ldc, M, N, K, g, p.nrounds, part,       \
+                     counters)
   switch (fl) {
     case 1: MM_LAUNCH_SK(1); break;
     case 2: MM_LAUNCH_SK(2); break;
@@ -480,9 +588,6 @@ int launch_skinny(const f16* A, int lda, const uint32_t* B, const f16* S, const 
   MM_CHECK_LAUNCH("gemm(skinny)");
   return 0;
 }
-
-
-
 
 #ifndef MM_ST_NW
 #define MM_ST_NW 8
@@ -568,22 +673,24 @@ size_t prefill_ws_bytes(int M, int N, int K) {
   return p.ksplit > 1 ? (size_t)p.ksplit * M * N * sizeof(float) : 0;
 }
 
-template <bool INT4, int WM, int WN, int RB, int CW>
-int launch_prefill2(const f16* A, int lda, const uint32_t* B, const f16* S, const f16* Z, f16* C,
-                    int ldc, int M, int N, int K, int g, int ks, float* part, hipStream_t st) {
+template <bool INT4, int ACT, int WM, int WN, int RB, int CW>
+int launch_prefill2(const f16* A, int lda, const uint32_t* B, const f16* S, const f16* Z,
+                    const uint32_t* B2, const f16* S2, const f16* Z2, f16* C, int ldc, int M,
+                    int N, int K, int g, int ks, float* part, hipStream_t st) {
   constexpr int BM = WM * 32 * RB, BN = WN * 32 * CW;
-  dim3 grid(mm_cdiv(N, BN), mm_cdiv(M, BM), ks);
+  dim3 grid(mm_cdiv(N, ACT == SK_PLAIN ? BN : BN / 2), mm_cdiv(M, BM), ks);
   if (g % PF2_BK == 0)
-    hipLaunchKernelGGL((k_prefill2<INT4, WM, WN, RB, CW, true>), grid, dim3(WM * WN * 64), 0, st,
-                       A, lda, B, S, Z, C, ldc, M, N, K, g, part);
+    hipLaunchKernelGGL((k_prefill2<INT4, WM, WN, RB, CW, true, ACT>), grid, dim3(WM * WN * 64), 0,
+                       st, A, lda, B, S, Z, B2, S2, Z2, C, ldc, M, N, K, g, part);
   else
-    hipLaunchKernelGGL((k_prefill2<INT4, WM, WN, RB, CW, false>), grid, dim3(WM * WN * 64), 0, st,
-                       A, lda, B, S, Z, C, ldc, M, N, K, g, part);
+    hipLaunchKernelGGL((k_prefill2<INT4, WM, WN, RB, CW, false, ACT>), grid, dim3(WM * WN * 64),
+                       0, st, A, lda, B, S, Z, B2, S2, Z2, C, ldc, M, N, K, g, part);
   MM_CHECK_LAUNCH("gemm(prefill2)");
   if (ks > 1) {
-    const size_t items = (size_t)M * (N / 4);
-    hipLaunchKernelGGL(k_splitk_reduce, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, st,
-                       part, ks, M, N, C, ldc);
+    const int OW = ACT == SK_PLAIN ? N : (ACT == SK_SWIGLU ? N : 2 * N);
+    const size_t items = (size_t)M * (OW / 4);
+    hipLaunchKernelGGL(k_splitk_reduce<ACT>, dim3((unsigned)((items + 255) / 256)), dim3(256), 0,
+                       st, part, ks, M, N, C, ldc);
     MM_CHECK_LAUNCH("gemm(prefill split-K reduce)");
   }
   return 0;
@@ -609,8 +716,12 @@ int gemm_dispatch(const char* who, const f16* A, const uint32_t* B, const f16* S
     if (MM_ST_MODE == 2 || ((long)K * N <= 4096L * 4096 && N / 16 >= 128))
       return launch_strip<INT4, 1>(A, K, B, S, Z, C, N, M, N, K, g, st);
   }
-  if (M <= 16) return launch_skinny<INT4, 1>(A, K, B, S, Z, C, N, M, N, K, g, ws, ws_bytes, st);
-  if (M <= 32) return launch_skinny<INT4, 2>(A, K, B, S, Z, C, N, M, N, K, g, ws, ws_bytes, st);
+  if (M <= 16)
+    return launch_skinny<INT4, 1, SK_PLAIN>(A, K, B, S, Z, nullptr, nullptr, nullptr, C, N, M, N,
+                                            K, g, ws, ws_bytes, st);
+  if (M <= 32)
+    return launch_skinny<INT4, 2, SK_PLAIN>(A, K, B, S, Z, nullptr, nullptr, nullptr, C, N, M, N,
+                                            K, g, ws, ws_bytes, st);
   // The pipelined kernel stages scale rows in 8-column pieces (N % 8 == 0)
   // and whole 64-k chunks (K % 64 == 0).
   if (MM_PF2_ENABLE && N % 8 == 0 && K % PF2_BK == 0) {
@@ -625,12 +736,15 @@ int gemm_dispatch(const char* who, const f16* A, const uint32_t* B, const f16* S
     }
     switch (p.cfg) {
       case 0:
-        return launch_prefill2<INT4, PF2_BIG>(A, K, B, S, Z, C, N, M, N, K, g, p.ksplit, part, st);
+        return launch_prefill2<INT4, SK_PLAIN, PF2_BIG>(A, K, B, S, Z, nullptr, nullptr, nullptr,
+                                                        C, N, M, N, K, g, p.ksplit, part, st);
       case 1:
-        return launch_prefill2<INT4, PF2_MID>(A, K, B, S, Z, C, N, M, N, K, g, p.ksplit, part, st);
+        return launch_prefill2<INT4, SK_PLAIN, PF2_MID>(A, K, B, S, Z, nullptr, nullptr, nullptr,
+                                                        C, N, M, N, K, g, p.ksplit, part, st);
       default:
-        return launch_prefill2<INT4, PF2_SMALL>(A, K, B, S, Z, C, N, M, N, K, g, p.ksplit, part,
-                                                st);
+        return launch_prefill2<INT4, SK_PLAIN, PF2_SMALL>(A, K, B, S, Z, nullptr, nullptr,
+                                                          nullptr, C, N, M, N, K, g, p.ksplit,
+                                                          part, st);
     }
   }
   // Prefill tiles: the largest tile that still gives about one block per CU.
@@ -639,6 +753,56 @@ int gemm_dispatch(const char* who, const f16* A, const uint32_t* B, const f16* S
     return launch_prefill<INT4, 2, 2, 4>(A, K, B, S, Z, C, N, M, N, K, g, st);
   if (M > 64) return launch_prefill<INT4, 2, 2, 2>(A, K, B, S, Z, C, N, M, N, K, g, st);
   return launch_prefill<INT4, 1, 2, 2>(A, K, B, S, Z, C, N, M, N, K, g, st);
+}
+
+// Gate/up pair product (ACT = SK_SWIGLU or SK_PAIR) over two [K/8, N] packed
+// matrices in one launch.  Decode sizes run the skinny kernel with one tile
+// of each matrix per block; prefill sizes the pipelined kernel with
+// tile-major gate/up columns.  Split-K and workspace are those of the
+// unfused [K, 2N] product.
+template <bool INT4, int ACT>
+int pair_dispatch(const char* who, const f16* A, const uint32_t* Bg, const f16* Sg,
+                  const f16* Zg, const uint32_t* Bu, const f16* Su, const f16* Zu, f16* C, int M,
+                  int N, int K, int g, void* ws, size_t ws_bytes, hipStream_t st) {
+  MM_CHECK_ARG(M >= 0 && N > 0 && K > 0, "%s: bad shape M=%d N=%d K=%d", who, M, N, K);
+  MM_CHECK_ARG(K % 8 == 0, "%s: K=%d must be divisible by 8", who, K);
+  MM_CHECK_ARG(N % 8 == 0, "%s: N=%d must be divisible by 8", who, N);
+  MM_CHECK_ARG(g > 0 && g % 8 == 0 && K % g == 0,
+               "%s: group_size=%d must be a multiple of 8 dividing K=%d", who, g, K);
+  MM_CHECK_ARG(M <= 32 || K % PF2_BK == 0, "%s: K=%d must be divisible by %d for M > 32", who, K,
+               PF2_BK);
+  const uintptr_t a16 = (uintptr_t)A | (uintptr_t)Bg | (uintptr_t)Bu | (uintptr_t)Sg |
+                        (uintptr_t)Su | (INT4 ? ((uintptr_t)Zg | (uintptr_t)Zu) : 0);
+  MM_CHECK_ARG((a16 & 15) == 0 && ((uintptr_t)C & 7) == 0,
+               "%s: A, packed weights, scales and zeros must be 16-byte aligned, C 8-byte", who);
+  if (M == 0) return 0;
+  const int ldc = ACT == SK_SWIGLU ? N : 2 * N;
+  if (M <= 16)
+    return launch_skinny<INT4, 1, ACT>(A, K, Bg, Sg, Zg, Bu, Su, Zu, C, ldc, M, N, K, g, ws,
+                                       ws_bytes, st);
+  if (M <= 32)
+    return launch_skinny<INT4, 2, ACT>(A, K, Bg, Sg, Zg, Bu, Su, Zu, C, ldc, M, N, K, g, ws,
+                                       ws_bytes, st);
+  const PrefillPlan p = plan_prefill(M, 2 * N, K);
+  float* part = nullptr;
+  if (p.ksplit > 1) {
+    const size_t need = SK_COUNTER_BYTES + prefill_ws_bytes(M, 2 * N, K);
+    MM_CHECK_ARG(ws != nullptr && ws_bytes >= need,
+                 "%s: workspace of %zu bytes is smaller than the %zu required", who, ws_bytes,
+                 need);
+    part = (float*)((char*)ws + SK_COUNTER_BYTES);
+  }
+  switch (p.cfg) {
+    case 0:
+      return launch_prefill2<INT4, ACT, PF2_BIG>(A, K, Bg, Sg, Zg, Bu, Su, Zu, C, ldc, M, N, K, g,
+                                                 p.ksplit, part, st);
+    case 1:
+      return launch_prefill2<INT4, ACT, PF2_MID>(A, K, Bg, Sg, Zg, Bu, Su, Zu, C, ldc, M, N, K, g,
+                                                 p.ksplit, part, st);
+    default:
+      return launch_prefill2<INT4, ACT, PF2_SMALL>(A, K, Bg, Sg, Zg, Bu, Su, Zu, C, ldc, M, N, K,
+                                                   g, p.ksplit, part, st);
+  }
 }
 
 }  // namespace
@@ -663,4 +827,17 @@ extern "C" int mm_u4_gemm(const uint16_t* A, const uint32_t* B, const uint16_t* 
                           size_t ws_bytes, void* stream) {
   return gemm_dispatch<true>("mm_u4_gemm", (const f16*)A, B, (const f16*)S, (const f16*)Z,
                              (f16*)C, M, N, K, g, ws, ws_bytes, (hipStream_t)stream);
+}
+
+extern "C" int mm_fp4_gate_up(const uint16_t* A, const uint32_t* Bg, const uint16_t* Sg,
+                              const uint32_t* Bu, const uint16_t* Su, uint16_t* C, int M, int N,
+                              int K, int g, int act, void* ws, size_t ws_bytes, void* stream) {
+  MM_CHECK_ARG(act == 0 || act == 1, "mm_fp4_gate_up: act=%d must be 0 or 1", act);
+  if (act == 1)
+    return pair_dispatch<false, SK_SWIGLU>("mm_fp4_gate_up", (const f16*)A, Bg, (const f16*)Sg,
+                                           nullptr, Bu, (const f16*)Su, nullptr, (f16*)C, M, N, K,
+                                           g, ws, ws_bytes, (hipStream_t)stream);
+  return pair_dispatch<false, SK_PAIR>("mm_fp4_gate_up", (const f16*)A, Bg, (const f16*)Sg,
+                                       nullptr, Bu, (const f16*)Su, nullptr, (f16*)C, M, N, K, g,
+                                       ws, ws_bytes, (hipStream_t)stream);
 }

@@ -192,9 +192,10 @@ k_moe_grouped(const f16* __restrict__ X, const int32_t* __restrict__ sorted_idx,
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[mt][t][j] = f32x4{0, 0, 0, 0};
     const f16* A = gather ? X : X + (size_t)mb * K;
-    skinny_wave<false, MT, NT, MOE_SPW, FL>(A, K, gather ? sorted_idx + mb : nullptr, topk, mrows, B,
-                                        S, nullptr, N, K, g, n0, coloff, wave * MOE_SPW, nrounds,
-                                        MOE_NW * MOE_SPW, acc);
+    const SkTile tl[NT] = {SkTile{B, S, nullptr, n0}, SkTile{B, S, nullptr, n0 + coloff}};
+    skinny_wave<false, MT, NT, MOE_SPW, FL>(A, K, gather ? sorted_idx + mb : nullptr, topk, mrows,
+                                            tl, N, K, g, wave * MOE_SPW, nrounds,
+                                            MOE_NW * MOE_SPW, acc);
     skinny_block_reduce<MT, NT, MOE_NW>(red, acc);
     if (wave == 0) {
 #pragma unroll
@@ -258,9 +259,12 @@ struct MoeSrc {
   }
   MM_DEV int col(int P, int w) const {
     if (!act) return min(o0 + P, ld - w);
-    const int oc = min(o0 + 32 * (P >> 6) + (P & 31), half - w);
-    return (P & 32) ? half + oc : oc;
+    const int oc = pair_out_col(o0, P, w, half);
+    return pair_is_up(P) ? half + oc : oc;
   }
+  MM_DEV const uint32_t* bcol(int P, int w) const { return B + col(P, w); }
+  MM_DEV const f16* scol(int P, int w) const { return S + col(P, w); }
+  MM_DEV const f16* zcol(int P, int w) const { return Z + col(P, w); }
 };
 
 template <int WM, int WN, int RB, bool G64>

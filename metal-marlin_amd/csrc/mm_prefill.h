@@ -25,6 +25,7 @@
 //               in one lane.
 #pragma once
 #include <type_traits>
+#include <utility>
 
 #include "mm_common.h"
 #include "mm_skinny.h"
@@ -33,8 +34,19 @@ namespace mmpf {
 using namespace mmsk;
 
 constexpr int PF2_BK = 64;
-constexpr int PF2_STAGES = 3;
-constexpr int PF2_SROWS = 8;
+#ifndef MM_PF2_STAGES
+#define MM_PF2_STAGES 3
+#endif
+#ifndef MM_PF2_SROWS
+#define MM_PF2_SROWS 8
+#endif
+constexpr int PF2_STAGES = MM_PF2_STAGES;   // LDS ring depth: loads run STAGES-1 chunks ahead
+constexpr int PF2_SROWS = MM_PF2_SROWS;     // scale rows staged per chunk (groups it may touch)
+
+template <class F, int... I>
+MM_DEV void static_for(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
@@ -78,9 +90,11 @@ struct Pf2Shape {
 // Runs chunks [c_beg, c_end) of 64 k into acc.  Source object `src`:
 //   src.arow(r)      -> const f16*, A row of tile row r (valid even past the
 //                       last row: clamp), element 0 = k 0;
-//   src.col(P, w)    -> global column of LDS column P, for a piece of w
-//                       (4 or 8) consecutive columns starting at P;
-//   src.B, src.S, src.Z, src.ld (row stride of B in words, S/Z in halves).
+//   src.bcol(P, w)   -> const uint32_t*, packed word row 0 of the global
+//                       column behind LDS column P, for a piece of w (4 or 8)
+//                       consecutive columns starting at P (clamped in range);
+//   src.scol(P, w), src.zcol(P, w) -> const f16*, the same for scales / zeros;
+//   src.ld           -> row stride of B in words and of S/Z in halves.
 // rb_live: the wave's row blocks past it hold no valid row and skip their
 // MFMAs (wave-uniform).  Requires K % 64 == 0.
 template <bool INT4, int WM, int WN, int RB, int CW, bool G64, bool TM, class Src>
@@ -111,15 +125,17 @@ MM_DEV void pf2_mainloop(const Src& src, int K, int g, int c_beg, int c_end, int
 #pragma unroll
   for (int i = 0; i < B_IT; ++i) {
     const int p = min((i * NWAVE + wave) * 64 + lane, Sh::B_PIECES - 1);
-    b_src[i] = src.B + (size_t)(p / (BN / 4)) * ld + src.col(4 * (p % (BN / 4)), 4);
+    b_src[i] = src.bcol(4 * (p % (BN / 4)), 4) + (size_t)(p / (BN / 4)) * ld;
   }
   int s_row[S_IT];
-  int s_col[S_IT];
+  const f16* s_src[S_IT];
+  const f16* z_src[S_IT];
 #pragma unroll
   for (int i = 0; i < S_IT; ++i) {
     const int p = min((i * NWAVE + wave) * 64 + lane, Sh::S_PIECES - 1);
     s_row[i] = p / (BN / 8);
-    s_col[i] = src.col(8 * (p % (BN / 8)), 8);
+    s_src[i] = src.scol(8 * (p % (BN / 8)), 8);
+    z_src[i] = INT4 ? src.zcol(8 * (p % (BN / 8)), 8) : nullptr;
   }
   auto issue = [&](int ch, int st) {
     const int k0 = ch * PF2_BK;
@@ -136,11 +152,11 @@ MM_DEV void pf2_mainloop(const Src& src, int K, int g, int c_beg, int c_end, int
 #pragma unroll
     for (int i = 0; i < S_IT; ++i) {
       const int wp = i * NWAVE + wave;
-      const size_t off = (size_t)min(gi0 + s_row[i], ngroups - 1) * ld + s_col[i];
+      const size_t off = (size_t)min(gi0 + s_row[i], ngroups - 1) * ld;
       const bool live = wp * 64 < Sh::S_PIECES;
-      gl2lds16(src.S + off, live ? smem + S_OFF + st * S_BYTES + wp * 1024 : smem + D_OFF);
+      gl2lds16(s_src[i] + off, live ? smem + S_OFF + st * S_BYTES + wp * 1024 : smem + D_OFF);
       if constexpr (INT4)
-        gl2lds16(src.Z + off, live ? smem + Z_OFF + st * S_BYTES + wp * 1024 : smem + D_OFF);
+        gl2lds16(z_src[i] + off, live ? smem + Z_OFF + st * S_BYTES + wp * 1024 : smem + D_OFF);
     }
   };
 
@@ -265,13 +281,26 @@ MM_DEV void pf2_mainloop(const Src& src, int K, int g, int c_beg, int c_end, int
       }
     }
   };
-  static_assert(PF2_STAGES == 3, "chunk loop is unrolled for three stages");
-  for (int ch = c_beg; ch < nch; ch += 3) {
-    chunk(ch, std::integral_constant<int, 0>{});
-    if (ch + 1 < nch) chunk(ch + 1, std::integral_constant<int, 1>{});
-    if (ch + 2 < nch) chunk(ch + 2, std::integral_constant<int, 2>{});
+  // The ring position of chunk ch is (ch - c_beg) % STAGES: unroll by STAGES so
+  // every LDS offset is a compile-time constant.
+  for (int ch = c_beg; ch < nch; ch += PF2_STAGES) {
+    static_for(
+        [&](auto stc) {
+          constexpr int st = decltype(stc)::value;
+          if (st == 0 || ch + st < nch) chunk(ch + st, stc);
+        },
+        std::make_integer_sequence<int, PF2_STAGES>{});
   }
   wait_vmcnt<0>();
 }
+
+// Column map of the tile-major (TM) pair kernels: each wave's 64 LDS columns
+// are 32 output columns twice, first from the gate matrix and then the same
+// columns from the up matrix.  Output column of LDS column P (o0 = the
+// block's first output column), clamped so a w-column piece stays in range.
+MM_DEV int pair_out_col(int o0, int P, int w, int nout) {
+  return min(o0 + 32 * (P >> 6) + (P & 31), nout - w);
+}
+MM_DEV bool pair_is_up(int P) { return (P & 32) != 0; }
 
 }  // namespace mmpf

@@ -55,18 +55,26 @@ MM_DEV const T* at_bytes(const void* base, uint32_t off) {
   return (const T*)((const char*)base + off);
 }
 
+// One 64-column tile of a packed weight matrix: its packed words, scales and
+// (INT4) zeros, all [.., N] with row stride N, and the tile's first column.
+// Tiles of one wave may come from different matrices of the same shape.
+struct SkTile {
+  const uint32_t* B;
+  const f16* S;
+  const f16* Z;
+  int col0;
+};
+
 // One wave's contribution over `nrounds` rounds of SPW consecutive 32-k steps:
-// round r covers steps st0 + r*ststride .. + SPW - 1.  NT column-tile quads
-// start at n0 + t*coloff.  FL: steps per scale flush (> 0, power of two,
-// <= SPW, and group_size == 32*FL*k for an integer k), or 0 for pre-scale.
+// round r covers steps st0 + r*ststride .. + SPW - 1, for NT column tiles.
+// FL: steps per scale flush (> 0, power of two, <= SPW, and
+// group_size == 32*FL*k for an integer k), or 0 for pre-scale.
 // Rows >= M and columns past N compute values that are never stored: their
 // addresses are clamped into the matrix so no load is predicated.
 template <bool INT4, int MT, int NT, int SPW, int FL>
 MM_DEV void skinny_wave(const f16* __restrict__ A, int lda, const int* __restrict__ rowmap,
-                        int rowdiv, int M, const uint32_t* __restrict__ B,
-                        const f16* __restrict__ S, const f16* __restrict__ Z, int N, int K, int g,
-                        int n0, int coloff, int st0, int nrounds, int ststride,
-                        f32x4 (&acc)[MT][NT][4]) {
+                        int rowdiv, int M, const SkTile (&tl)[NT], int N, int K, int g,
+                        int st0, int nrounds, int ststride, f32x4 (&acc)[MT][NT][4]) {
   static_assert(FL == 0 || (SPW % FL == 0), "flush interval must divide the round");
   const int lane = threadIdx.x & 63;
   const int c = lane & 15, q = lane >> 4;
@@ -82,7 +90,7 @@ MM_DEV void skinny_wave(const f16* __restrict__ A, int lda, const int* __restric
   }
   uint32_t coff[NT];                       // column index of this lane's first column
 #pragma unroll
-  for (int t = 0; t < NT; ++t) coff[t] = (uint32_t)min(n0 + t * coloff + 4 * c, N - 4);
+  for (int t = 0; t < NT; ++t) coff[t] = (uint32_t)min(tl[t].col0 + 4 * c, N - 4);
 
   for (int r = 0; r < nrounds; ++r) {
     const int stb = st0 + r * ststride;    // wave-uniform
@@ -95,7 +103,7 @@ MM_DEV void skinny_wave(const f16* __restrict__ A, int lda, const int* __restric
       const int kp = min(4 * min(stb + i, nsteps - 1) + q, KP - 1);
 #pragma unroll
       for (int t = 0; t < NT; ++t)
-        w[i][t] = *at_bytes<u32x4>(B, ((uint32_t)kp * (uint32_t)N + coff[t]) * 4u);
+        w[i][t] = *at_bytes<u32x4>(tl[t].B, ((uint32_t)kp * (uint32_t)N + coff[t]) * 4u);
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
         a[i][mt] = *at_bytes<f16x8>(A, aoff[mt] + (uint32_t)kp * 16u);
@@ -120,9 +128,9 @@ MM_DEV void skinny_wave(const f16* __restrict__ A, int lda, const int* __restric
         const uint32_t gi = (uint32_t)((kp * 8) / g);
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-          const f16x4 s4 = *at_bytes<f16x4>(S, (gi * (uint32_t)N + coff[t]) * 2u);
+          const f16x4 s4 = *at_bytes<f16x4>(tl[t].S, (gi * (uint32_t)N + coff[t]) * 2u);
           f16x4 z4 = {0, 0, 0, 0};
-          if constexpr (INT4) z4 = *at_bytes<f16x4>(Z, (gi * (uint32_t)N + coff[t]) * 2u);
+          if constexpr (INT4) z4 = *at_bytes<f16x4>(tl[t].Z, (gi * (uint32_t)N + coff[t]) * 2u);
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             f16 nz = 0;
@@ -144,8 +152,8 @@ MM_DEV void skinny_wave(const f16* __restrict__ A, int lda, const int* __restric
         f16x4 s4[NT], z4[NT];
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-          s4[t] = *at_bytes<f16x4>(S, (gi * (uint32_t)N + coff[t]) * 2u);
-          if constexpr (INT4) z4[t] = *at_bytes<f16x4>(Z, (gi * (uint32_t)N + coff[t]) * 2u);
+          s4[t] = *at_bytes<f16x4>(tl[t].S, (gi * (uint32_t)N + coff[t]) * 2u);
+          if constexpr (INT4) z4[t] = *at_bytes<f16x4>(tl[t].Z, (gi * (uint32_t)N + coff[t]) * 2u);
         }
         f32x4 grp[MT][NT][4];
 #pragma unroll

@@ -3,9 +3,10 @@ path with the Python surface of RESMP-DEV/metal-marlin's quantized linear,
 kernels and moe_dispatch modules.  Kernels live in libmmfp4.so (HIP, C ABI)."""
 
 from .kernels import (FP4_PER_UINT, decode_gemv_fp4, dequant_fp4, dequant_fp4_decode_gemv,
-                      dequant_int4, dequantize_mmfp4, marlin_gemm_fp4, marlin_gemm_fp4_tuned,
-                      marlin_gemm_fused_fp4, marlin_gemm_fused_u4, marlin_gemm_int4, mmfp4_gemm,
-                      select_decode_kernel)
+                      dequant_int4, dequantize_mmfp4, fused_gate_up_gemm, marlin_gemm_fp4,
+                      marlin_gemm_fp4_tuned, marlin_gemm_fused_fp4, marlin_gemm_fused_u4,
+                      marlin_gemm_int4, mmfp4_fused_gate_up, mmfp4_fused_gate_up_marlin,
+                      mmfp4_gemm, select_decode_kernel)
 from .moe_dispatch import (MoEDispatcher, MoEDispatchInfo, compute_expert_load,
                            compute_load_balancing_loss, gather_for_experts,
                            group_tokens_by_expert, group_tokens_by_expert_full,

@@ -17,7 +17,8 @@ __all__ = [
     "marlin_gemm_fp4", "marlin_gemm_fp4_tuned", "marlin_gemm_fused_fp4",
     "marlin_gemm_int4", "marlin_gemm_fused_u4", "dequant_fp4", "dequant_int4",
     "dequant_fp4_decode_gemv", "decode_gemv_fp4", "mmfp4_gemm", "dequantize_mmfp4",
-    "select_decode_kernel", "FP4_PER_UINT",
+    "select_decode_kernel", "fused_gate_up_gemm", "mmfp4_fused_gate_up",
+    "mmfp4_fused_gate_up_marlin", "FP4_PER_UINT",
 ]
 
 FP4_PER_UINT = 8
@@ -103,6 +104,84 @@ def marlin_gemm_int4(A: torch.Tensor, B_packed: torch.Tensor, scales: torch.Tens
 def marlin_gemm_fused_u4(A, B_packed, scales, zeros, group_size: int = 32):
     """Alias of marlin_gemm_int4 (kernels_core.py:2068-2077)."""
     return marlin_gemm_int4(A, B_packed, scales, zeros, group_size)
+
+
+def _gate_up(x: torch.Tensor, gate_packed: torch.Tensor, gate_scales: torch.Tensor,
+             up_packed: torch.Tensor, up_scales: torch.Tensor, group_size: int,
+             act: int) -> torch.Tensor:
+    """One launch over the gate and up matrices, both Marlin [K/8, N]:
+    act=1 -> silu(x @ Wg) * (x @ Wu) [M, N]; act=0 -> [x @ Wg | x @ Wu] [M, 2N]."""
+    dev = _lib.require_device(x, gate_packed, gate_scales, up_packed, up_scales)
+    if x.dim() != 2:
+        raise ValueError(f"x must be 2D [M, K], got shape={tuple(x.shape)}")
+    M, K = x.shape
+    K_packed, N = gate_packed.shape
+    if tuple(up_packed.shape) != (K_packed, N):
+        raise ValueError("up_packed must match gate_packed shape "
+                         f"({K_packed}, {N}), got {tuple(up_packed.shape)}")
+    if K != K_packed * FP4_PER_UINT:
+        raise ValueError(f"K mismatch: x has K={K}, but packed tensors imply "
+                         f"K={K_packed * FP4_PER_UINT}")
+    _check_groups("gate_scales", gate_scales, K, N, group_size)
+    _check_groups("up_scales", up_scales, K, N, group_size)
+    a = _half(x)
+    out = torch.empty((M, N if act else 2 * N), dtype=torch.float16, device=dev)
+    ws_bytes = int(_lib.load().mm_gemm_workspace_bytes(M, 2 * N, K))
+    ws = _lib.workspace(dev, ws_bytes)
+    gp, up = _packed(gate_packed), _packed(up_packed)
+    gs, us = _half(gate_scales), _half(up_scales)
+    _lib.call("mm_fp4_gate_up", _lib.ptr(a), _lib.ptr(gp), _lib.ptr(gs), _lib.ptr(up),
+              _lib.ptr(us), _lib.ptr(out), M, N, K, group_size, act, _lib.ptr(ws), ws.numel(),
+              _lib.stream_of(a))
+    return out
+
+
+def fused_gate_up_gemm(x: torch.Tensor, gate_packed: torch.Tensor, gate_scales: torch.Tensor,
+                       up_packed: torch.Tensor, up_scales: torch.Tensor,
+                       group_size: int = 128) -> torch.Tensor:
+    """Gate and up projections in one launch (kernels_core.py:4749-4760 ->
+    MetalKernels.fused_gate_up_gemm :4220-4267): packed [K/8, N] Marlin
+    layout, scales [K/group_size, N]; returns [M, 2N] fp16 with the gate
+    product in columns [0, N) and the up product in [N, 2N)."""
+    return _gate_up(x, gate_packed, gate_scales, up_packed, up_scales, group_size, 0)
+
+
+def mmfp4_fused_gate_up(x: torch.Tensor, gate_packed: torch.Tensor, gate_scales: torch.Tensor,
+                        up_packed: torch.Tensor, up_scales: torch.Tensor,
+                        group_size: int = 128) -> torch.Tensor:
+    """silu(gate_proj(x)) * up_proj(x) (kernels_core.py:4762-4774 ->
+    MetalKernels.mmfp4_fused_gate_up :4269-4408).  Layout as documented there:
+    gate_packed / up_packed row-packed [N, K/8] uint32, scales [K/group_size, N].
+    The row-packed words are transposed to the Marlin layout on the device for
+    each call (as the reference's own M < 64 path does); callers that keep the
+    Marlin layout call `mmfp4_fused_gate_up_marlin` and skip the transpose.
+    SiLU is applied to the fp32 sums (the reference rounds them to fp16 first)."""
+    if x.dim() != 2:
+        raise ValueError(f"x must be 2D [M, K], got shape={tuple(x.shape)}")
+    M, K = x.shape
+    N, K_packed = gate_packed.shape
+    if tuple(up_packed.shape) != (N, K_packed):
+        raise ValueError("up_packed must match gate_packed shape "
+                         f"({N}, {K_packed}), got {tuple(up_packed.shape)}")
+    if K != K_packed * FP4_PER_UINT:
+        raise ValueError(f"K mismatch: x has K={K}, but packed tensors imply "
+                         f"K={K_packed * FP4_PER_UINT}")
+    if K % group_size != 0:
+        raise ValueError(f"K ({K}) must be divisible by group_size ({group_size})")
+    expected = (K // group_size, N)
+    for name, sc in (("gate_scales", gate_scales), ("up_scales", up_scales)):
+        if tuple(sc.shape) != expected:
+            raise ValueError(f"{name} shape mismatch: expected {expected}, got {tuple(sc.shape)}")
+    return _gate_up(x, _packed(gate_packed).t().contiguous(), gate_scales,
+                    _packed(up_packed).t().contiguous(), up_scales, group_size, 1)
+
+
+def mmfp4_fused_gate_up_marlin(x: torch.Tensor, gate_packed: torch.Tensor,
+                               gate_scales: torch.Tensor, up_packed: torch.Tensor,
+                               up_scales: torch.Tensor, group_size: int = 128) -> torch.Tensor:
+    """mmfp4_fused_gate_up on Marlin-layout [K/8, N] weights (no transpose):
+    silu(x @ Wg) * (x @ Wu) -> [M, N] fp16 in one launch."""
+    return _gate_up(x, gate_packed, gate_scales, up_packed, up_scales, group_size, 1)
 
 
 def dequant_fp4(B_packed: torch.Tensor, scales: torch.Tensor, K: int, N: int,
