@@ -93,6 +93,18 @@ int mm_fp4_gate_up(const uint16_t* A, const uint32_t* Bg, const uint16_t* Sg, co
                    const uint16_t* Su, uint16_t* C, int M, int N, int K, int group_size, int act,
                    void* ws, size_t ws_bytes, void* stream);
 
+/* Up to three FP4 products sharing A and K, one output each:
+ * C[p] [M, N[p]] = A . dequant(B[p], S[p]), p < nmat <= 3 (B[p] Marlin
+ * [K/8, N[p]], S[p] [K/g, N[p]]).  The tables are host arrays of device
+ * pointers.  M <= 16 runs one launch over all the matrices' column tiles; larger
+ * M runs one launch per matrix.  Replaces metal_marlin/kernels_core.py:4875-4948
+ * (mmfp4_fused_qkv) and the Metal shaders/mmfp4_fused_qkv.metal dispatch.
+ * Workspace: the larger of mm_gemm_workspace_bytes(M, sum N[p], K) and each
+ * mm_gemm_workspace_bytes(M, N[p], K).  Other requirements as mm_fp4_gemm. */
+int mm_fp4_gemm_multi(const uint16_t* A, int nmat, const uint32_t* const* B,
+                      const uint16_t* const* S, uint16_t* const* C, const int* N, int M, int K,
+                      int group_size, void* ws, size_t ws_bytes, void* stream);
+
 /* -------------------------------------------------------------------- MoE */
 
 /* Stable counting sort of the T*k (token, slot) assignments by expert.

@@ -37,31 +37,62 @@ MM_DEV float swiglu(float gate, float up) { return gate / (1.0f + __expf(-gate))
 //   SK_PLAIN : C[:, n] = A . W[:, n]                          (one matrix)
 //   SK_SWIGLU: C[:, n] = silu(A . Wg[:, n]) * (A . Wu[:, n])   (gate, up; C is [M, N])
 //   SK_PAIR  : C[:, n] = A . Wg[:, n], C[:, N + n] = A . Wu[:, n]   (C is [M, 2N])
-enum { SK_PLAIN = 0, SK_SWIGLU = 1, SK_PAIR = 2 };
+//   SK_MULTI : up to three independent products sharing A and K (Q, K, V):
+//              the grid's column tiles are the three matrices' tiles in turn.
+enum { SK_PLAIN = 0, SK_SWIGLU = 1, SK_PAIR = 2, SK_MULTI = 3 };
 
-// Dense skinny kernel.  grid = (column tiles, ksplit).  SK_PLAIN: a block
-// covers NT adjacent 64-column tiles of B.  SK_SWIGLU / SK_PAIR (NT = 2):
-// tile 0 is columns [n0, n0+64) of (B, S, Z) and tile 1 the same columns of
-// (B2, S2, Z2).  Split-K partials are [ksplit][M][PW] fp32 with PW = N, or
-// 2N for the pair modes (gate at n, up at N + n).
+// SK_MULTI problem table: matrix p owns column tiles [tile0[p], tile0[p+1])
+// and partial-sum columns [cbase[p], cbase[p] + N[p]) of a [ksplit][M][ntot]
+// buffer; C[p] is [M, N[p]].
+struct SkMulti {
+  const uint32_t* B[3];
+  const f16* S[3];
+  const f16* Z[3];
+  f16* C[3];
+  int N[3];
+  int tile0[4];
+  int cbase[3];
+  int ntot;
+};
+
+// Dense skinny kernel.  grid = (column tiles, ksplit).  SK_PLAIN / SK_MULTI:
+// a block covers NT adjacent 64-column tiles of one matrix.  SK_SWIGLU /
+// SK_PAIR (NT = 2): tile 0 is columns [n0, n0+64) of (B, S, Z) and tile 1
+// the same columns of (B2, S2, Z2).  Split-K partials are [ksplit][M][PW]
+// fp32 with PW = N, 2N for the pair modes (gate at n, up at N + n), or ntot.
 template <bool INT4, int MT, int NT, int SPW, int NW, int FL, int ACT>
 __global__ void __launch_bounds__(NW * 64)
 k_skinny(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
          const f16* __restrict__ S, const f16* __restrict__ Z, const uint32_t* __restrict__ B2,
          const f16* __restrict__ S2, const f16* __restrict__ Z2, f16* __restrict__ C, int ldc,
          int M, int N, int K, int g, int nrounds, float* __restrict__ part,
-         uint32_t* __restrict__ counters) {
-  static_assert(ACT == SK_PLAIN || NT == 2, "pair modes use one tile of each matrix");
+         uint32_t* __restrict__ counters, SkMulti mp) {
+  static_assert(ACT == SK_PLAIN || ACT == SK_MULTI || NT == 2,
+                "pair modes use one tile of each matrix");
+  constexpr bool ONE = ACT == SK_PLAIN || ACT == SK_MULTI;   // one matrix per block
   constexpr int RED = (NW > 1 ? NW - 1 : 1) * MT * NT * 16 * 64;
   __shared__ float red[RED];
   __shared__ uint32_t s_last;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int c = lane & 15, q = lane >> 4;
-  const int n0 = blockIdx.x * (ACT == SK_PLAIN ? NT : 1) * SK_COLS;
+  int tile = blockIdx.x, cbase = 0, PW = ONE ? N : 2 * N;
+  if constexpr (ACT == SK_MULTI) {
+    const int p = tile >= mp.tile0[2] ? 2 : (tile >= mp.tile0[1] ? 1 : 0);
+    B = mp.B[p];
+    S = mp.S[p];
+    Z = mp.Z[p];
+    C = mp.C[p];
+    N = mp.N[p];
+    ldc = N;
+    tile -= mp.tile0[p];
+    cbase = mp.cbase[p];
+    PW = mp.ntot;
+  }
+  const int n0 = tile * (ONE ? NT : 1) * SK_COLS;
   const int ksplit = gridDim.y;
-  const int PW = ACT == SK_PLAIN ? N : 2 * N;
-  // Column of tile t (lane group c) in the partial-sum row, and in C.
-  auto pcol = [&](int t) { return ACT == SK_PLAIN ? n0 + t * SK_COLS + 4 * c : t * N + n0 + 4 * c; };
+  // First column (lane group c) of tile t in C and in the partial-sum row.
+  auto ccol = [&](int t) { return ONE ? n0 + t * SK_COLS + 4 * c : n0 + 4 * c + (ACT == SK_PAIR ? t * N : 0); };
+  auto pcol = [&](int t) { return ONE ? cbase + n0 + t * SK_COLS + 4 * c : t * N + n0 + 4 * c; };
   // Steps owned by this block: NW*SPW*nrounds consecutive 32-k steps; waves
   // take interleaved SPW-step slabs so each round reads adjacent word rows.
   const int blk_st0 = blockIdx.y * NW * SPW * nrounds;
@@ -76,8 +107,8 @@ k_skinny(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
   SkTile tl[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t)
-    tl[t] = ACT == SK_PLAIN ? SkTile{B, S, Z, n0 + t * SK_COLS}
-                            : (t == 0 ? SkTile{B, S, Z, n0} : SkTile{B2, S2, Z2, n0});
+    tl[t] = ONE ? SkTile{B, S, Z, n0 + t * SK_COLS}
+                : (t == 0 ? SkTile{B, S, Z, n0} : SkTile{B2, S2, Z2, n0});
   skinny_wave<INT4, MT, NT, SPW, FL>(A, lda, nullptr, 1, M, tl, N, K, g, blk_st0 + wave * SPW,
                                      nrounds, NW * SPW, acc);
   skinny_block_reduce<MT, NT, NW>(red, acc);
@@ -103,9 +134,9 @@ k_skinny(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
         } else {
 #pragma unroll
           for (int t = 0; t < NT; ++t) {
-            const int col = ACT == SK_PLAIN ? n0 + t * SK_COLS + 4 * c : n0 + 4 * c;
+            const int col = ONE ? n0 + t * SK_COLS + 4 * c : n0 + 4 * c;
             if (col < N)
-              *(f16x4*)(C + (size_t)row * ldc + pcol(t)) =
+              *(f16x4*)(C + (size_t)row * ldc + ccol(t)) =
                   f16x4{(f16)acc[mt][t][0][rr], (f16)acc[mt][t][1][rr], (f16)acc[mt][t][2][rr],
                         (f16)acc[mt][t][3][rr]};
           }
@@ -123,7 +154,7 @@ k_skinny(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
-        const int col = ACT == SK_PLAIN ? n0 + t * SK_COLS + 4 * c : n0 + 4 * c;
+        const int col = ONE ? n0 + t * SK_COLS + 4 * c : n0 + 4 * c;
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
           const int row = mt * 16 + 4 * q + rr;
@@ -183,11 +214,11 @@ k_skinny(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
                 (f16)swiglu(gt[2], up[2]), (f16)swiglu(gt[3], up[3])};
     } else {
       const int t = gi / (SK_COLS / 4);
-      const int col = (ACT == SK_PLAIN ? n0 + t * SK_COLS : n0) + 4 * (gi % (SK_COLS / 4));
+      const int col = (ONE ? n0 + t * SK_COLS : n0) + 4 * (gi % (SK_COLS / 4));
       if (col >= N) continue;
-      const int pc = ACT == SK_PLAIN ? col : t * N + col;
-      const f32x4 v = sum_splits(row, pc);
-      *(f16x4*)(C + (size_t)row * ldc + pc) = f16x4{(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
+      const int oc = ONE ? col : t * N + col;
+      const f32x4 v = sum_splits(row, ONE ? cbase + col : oc);
+      *(f16x4*)(C + (size_t)row * ldc + oc) = f16x4{(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
     }
   }
   if (threadIdx.x == 0)
@@ -552,14 +583,17 @@ size_t skinny_ws_bytes(int M, int N, int K) {
 // ACT = SK_PLAIN: C = A . B.  Pair modes: B/S/Z is the gate matrix and
 // B2/S2/Z2 the up matrix, both [.., N]; the split and workspace are those of
 // the unfused [K, 2N] product (plan_skinny(M, 2N, K)).
+// SK_MULTI: `mp` describes the matrices (N is then mp->ntot, B..Z2 unused).
 template <bool INT4, int MT, int ACT>
 int launch_skinny(const f16* A, int lda, const uint32_t* B, const f16* S, const f16* Z,
                   const uint32_t* B2, const f16* S2, const f16* Z2, f16* C, int ldc, int M,
-                  int N, int K, int g, void* ws, size_t ws_bytes, hipStream_t st) {
-  const int PW = ACT == SK_PLAIN ? N : 2 * N;
+                  int N, int K, int g, void* ws, size_t ws_bytes, hipStream_t st,
+                  const SkMulti* mp = nullptr) {
+  const int PW = ACT == SK_PLAIN || ACT == SK_MULTI ? N : 2 * N;
   const SkinnyPlan p = plan_skinny(M, PW, K);
-  constexpr int NT = ACT == SK_PLAIN ? sk_nt<MT>() : 2;
-  const int gx = ACT == SK_PLAIN ? p.ntiles : mm_cdiv(N, SK_COLS);
+  constexpr int NT = ACT == SK_PLAIN || ACT == SK_MULTI ? sk_nt<MT>() : 2;
+  const int gx = ACT == SK_PLAIN ? p.ntiles : (ACT == SK_MULTI ? mp->tile0[3] : mm_cdiv(N, SK_COLS));
+  const SkMulti none{};
   MM_CHECK_ARG(gx <= SK_MAX_TILES, "gemm: N=%d exceeds the supported %d columns", N,
                SK_MAX_TILES * SK_COLS);
   uint32_t* counters = (uint32_t*)ws;
@@ -576,7 +610,7 @@ int launch_skinny(const f16* A, int lda, const uint32_t* B, const f16* S, const 
 #define MM_LAUNCH_SK(FLV)                                                                   \
   hipLaunchKernelGGL((k_skinny<INT4, MT, NT, SPW, SK_NW, FLV, ACT>), grid, dim3(SK_NW * 64), 0, \
                      st, A, lda, B, S, Z, B2, S2, Z2, C, ldc, M, N, K, g, p.nrounds, part,       \
-                     counters)
+                     counters, mp ? *mp : none)
   switch (fl) {
     case 1: MM_LAUNCH_SK(1); break;
     case 2: MM_LAUNCH_SK(2); break;
@@ -805,6 +839,53 @@ int pair_dispatch(const char* who, const f16* A, const uint32_t* Bg, const f16* 
   }
 }
 
+// Up to three FP4 products sharing A (the Q, K and V projections): decode
+// sizes run one SK_MULTI launch over all their column tiles; larger M runs
+// one launch per matrix.
+int multi_dispatch(const char* who, const f16* A, int nmat, const uint32_t* const* B,
+                   const f16* const* S, f16* const* C, const int* N, int M, int K, int g,
+                   void* ws, size_t ws_bytes, hipStream_t st) {
+  MM_CHECK_ARG(nmat >= 1 && nmat <= 3, "%s: nmat=%d must be 1..3", who, nmat);
+  MM_CHECK_ARG(B != nullptr && S != nullptr && C != nullptr && N != nullptr,
+               "%s: null matrix table", who);
+  MM_CHECK_ARG(M >= 0 && K > 0, "%s: bad shape M=%d K=%d", who, M, K);
+  SkMulti mp{};
+  int ntot = 0, tiles = 0;
+  for (int p = 0; p < nmat; ++p) {
+    MM_CHECK_ARG(N[p] > 0 && N[p] % 4 == 0, "%s: N[%d]=%d must be a positive multiple of 4",
+                 who, p, N[p]);
+    mp.B[p] = B[p];
+    mp.S[p] = S[p];
+    mp.C[p] = C[p];
+    mp.N[p] = N[p];
+    mp.tile0[p] = tiles;
+    mp.cbase[p] = ntot;
+    tiles += mm_cdiv(N[p], SK_COLS);
+    ntot += N[p];
+  }
+  for (int p = nmat; p < 3; ++p) mp.tile0[p] = tiles;
+  mp.tile0[3] = tiles;
+  mp.ntot = ntot;
+  if (M > 16 || flush_steps(g, sk_spw<1>()) == 0 || K % 8 != 0 || g <= 0 || K % g != 0) {
+    // One product per launch (M > 16, or shapes the GEMM entry rejects with
+    // its own message).
+    for (int p = 0; p < nmat; ++p) {
+      const int rc = gemm_dispatch<false>(who, A, B[p], S[p], nullptr, C[p], M, N[p], K, g, ws,
+                                          ws_bytes, st);
+      if (rc != 0) return rc;
+    }
+    return 0;
+  }
+  uintptr_t al = (uintptr_t)A;
+  for (int p = 0; p < nmat; ++p) al |= (uintptr_t)B[p] | ((uintptr_t)S[p] & 7) | ((uintptr_t)C[p] & 7);
+  MM_CHECK_ARG((al & 15) == 0, "%s: A, B 16-byte / scales, C 8-byte alignment required", who);
+  MM_CHECK_ARG(tiles <= SK_MAX_TILES, "%s: too many columns", who);
+  if (M == 0) return 0;
+  return launch_skinny<false, 1, SK_MULTI>(A, K, nullptr, nullptr, nullptr, nullptr, nullptr,
+                                           nullptr, nullptr, 0, M, ntot, K, g, ws, ws_bytes, st,
+                                           &mp);
+}
+
 }  // namespace
 
 // ===========================================================================
@@ -840,4 +921,11 @@ extern "C" int mm_fp4_gate_up(const uint16_t* A, const uint32_t* Bg, const uint1
   return pair_dispatch<false, SK_PAIR>("mm_fp4_gate_up", (const f16*)A, Bg, (const f16*)Sg,
                                        nullptr, Bu, (const f16*)Su, nullptr, (f16*)C, M, N, K, g,
                                        ws, ws_bytes, (hipStream_t)stream);
+}
+
+extern "C" int mm_fp4_gemm_multi(const uint16_t* A, int nmat, const uint32_t* const* B,
+                                 const uint16_t* const* S, uint16_t* const* C, const int* N, int M,
+                                 int K, int g, void* ws, size_t ws_bytes, void* stream) {
+  return multi_dispatch("mm_fp4_gemm_multi", (const f16*)A, nmat, B, (const f16* const*)S,
+                        (f16* const*)C, N, M, K, g, ws, ws_bytes, (hipStream_t)stream);
 }

@@ -6,6 +6,7 @@ from .kernels import (FP4_PER_UINT, decode_gemv_fp4, dequant_fp4, dequant_fp4_de
                       dequant_int4, dequantize_mmfp4, fused_gate_up_gemm, marlin_gemm_fp4,
                       marlin_gemm_fp4_tuned, marlin_gemm_fused_fp4, marlin_gemm_fused_u4,
                       marlin_gemm_int4, mmfp4_fused_gate_up, mmfp4_fused_gate_up_marlin,
+                      mmfp4_fused_qkv,
                       mmfp4_gemm, select_decode_kernel)
 from .moe_dispatch import (MoEDispatcher, MoEDispatchInfo, compute_expert_load,
                            compute_load_balancing_loss, gather_for_experts,

@@ -31,6 +31,8 @@ SIGNATURES: dict[str, tuple] = {
                             _c_size, _vp]),
     "mm_fp4_gate_up": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int,
                                 _c_int, _vp, _c_size, _vp]),
+    "mm_fp4_gemm_multi": (_c_int, [_vp, _c_int, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp,
+                                   _c_size, _vp]),
     "mm_moe_sort": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp]),
     "mm_moe_sort_i64": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp]),
     "mm_moe_grouped_gemm": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _vp, _c_int,

@@ -18,7 +18,7 @@ __all__ = [
     "marlin_gemm_int4", "marlin_gemm_fused_u4", "dequant_fp4", "dequant_int4",
     "dequant_fp4_decode_gemv", "decode_gemv_fp4", "mmfp4_gemm", "dequantize_mmfp4",
     "select_decode_kernel", "fused_gate_up_gemm", "mmfp4_fused_gate_up",
-    "mmfp4_fused_gate_up_marlin", "FP4_PER_UINT",
+    "mmfp4_fused_gate_up_marlin", "mmfp4_fused_qkv", "FP4_PER_UINT",
 ]
 
 FP4_PER_UINT = 8
@@ -182,6 +182,47 @@ def mmfp4_fused_gate_up_marlin(x: torch.Tensor, gate_packed: torch.Tensor,
     """mmfp4_fused_gate_up on Marlin-layout [K/8, N] weights (no transpose):
     silu(x @ Wg) * (x @ Wu) -> [M, N] fp16 in one launch."""
     return _gate_up(x, gate_packed, gate_scales, up_packed, up_scales, group_size, 1)
+
+
+def mmfp4_fused_qkv(A: torch.Tensor, Q_packed: torch.Tensor, Q_scales: torch.Tensor,
+                    K_packed: torch.Tensor, K_scales: torch.Tensor, V_packed: torch.Tensor,
+                    V_scales: torch.Tensor, group_size: int = 128):
+    """Q, K, V projections sharing A (kernels_core.py:4875-4948):
+    Q = A @ dequant(Q_packed, Q_scales), and likewise K and V; packed
+    [K/8, N*] Marlin layout, scales [K/group_size, N*].  Returns (Q, K, V)
+    fp16 [M, Nq], [M, Nk], [M, Nv] (shaped like A's leading dims).  M <= 16
+    runs one launch over all three matrices' column tiles; larger M runs one
+    launch per matrix (the reference falls back to separate GEMMs for M > 1)."""
+    dev = _lib.require_device(A, Q_packed, Q_scales, K_packed, K_scales, V_packed, V_scales)
+    orig_shape = A.shape
+    if A.dim() == 1:
+        A = A.reshape(1, -1)
+    Kdim = A.shape[-1]
+    M = A.numel() // Kdim
+    mats = []
+    for name, p, sc in (("Q", Q_packed, Q_scales), ("K", K_packed, K_scales),
+                        ("V", V_packed, V_scales)):
+        if p.dim() != 2 or p.shape[0] * FP4_PER_UINT != Kdim:
+            raise ValueError(f"{name} weights: K mismatch {Kdim} vs "
+                             f"{p.shape[0] * FP4_PER_UINT if p.dim() == 2 else '?'}")
+        _check_groups(f"{name}_scales", sc, Kdim, p.shape[1], group_size)
+        mats.append((_packed(p), _half(sc)))
+    a = _half(A.reshape(M, Kdim))
+    Ns = [p.shape[1] for p, _ in mats]
+    outs = [torch.empty((M, n), dtype=torch.float16, device=dev) for n in Ns]
+    lib = _lib.load()
+    ws_bytes = max([int(lib.mm_gemm_workspace_bytes(M, sum(Ns), Kdim))] +
+                   [int(lib.mm_gemm_workspace_bytes(M, n, Kdim)) for n in Ns])
+    ws = _lib.workspace(dev, ws_bytes)
+    import ctypes
+    Bt = (ctypes.c_void_p * 3)(*[_lib.ptr(p) for p, _ in mats])
+    St = (ctypes.c_void_p * 3)(*[_lib.ptr(sc) for _, sc in mats])
+    Ct = (ctypes.c_void_p * 3)(*[_lib.ptr(o) for o in outs])
+    Nt = (ctypes.c_int * 3)(*Ns)
+    _lib.call("mm_fp4_gemm_multi", _lib.ptr(a), 3, Bt, St, Ct, Nt, M, Kdim, group_size,
+              _lib.ptr(ws), ws.numel(), _lib.stream_of(a))
+    lead = tuple(orig_shape[:-1]) if len(orig_shape) > 1 else (1,)
+    return tuple(o.reshape(*lead, n) for o, n in zip(outs, Ns))
 
 
 def dequant_fp4(B_packed: torch.Tensor, scales: torch.Tensor, K: int, N: int,
