@@ -157,6 +157,80 @@ def run_single_bench(torch, mmfp4, M: int, K: int, N: int, steps: int):
             "TBps": round(alg_bytes(M, K, N) / (us * 1e-6) / 1e12, 3)}
 
 
+def rand_weights(torch, K: int, N: int, gen):
+    """Random packed words and scales of the right shape (timing only: the
+    kernels' cost does not depend on the values)."""
+    p = torch.randint(-2**31, 2**31 - 1, (K // 8, N), generator=gen, dtype=torch.int32,
+                      device="cuda")
+    s = (torch.rand((K // G, N), generator=gen, device="cuda") * 0.01).half()
+    return p, s
+
+
+def run_fused_bench(torch, mmfp4, steps: int):
+    """SURVEY next rows at the Llama-3-8B shapes, fused vs unfused, rotated
+    weight copies: gate_up+SiLU (4096 -> 2 x 14336) at M=1 and M=2048, and
+    the Q/K/V projections (4096 -> 4096 + 1024 + 1024) at M=1."""
+    gen = torch.Generator(device="cuda").manual_seed(900)
+    res = {}
+    K, N = 4096, 14336
+    copies = max(2, -(-ROTATE_BYTES // (2 * alg_bytes(0, K, N))))
+    gu = [(rand_weights(torch, K, N, gen), rand_weights(torch, K, N, gen)) for _ in range(copies)]
+    cat = [(torch.cat([g[0], u[0]], 1), torch.cat([g[1], u[1]], 1)) for g, u in gu]
+    for M, st in ((1, steps), (2048, max(3, steps // 40))):
+        a = torch.randn((M, K), generator=gen, device="cuda").half()
+        fused = [[lambda w=w: mmfp4.mmfp4_fused_gate_up_marlin(a, w[0][0], w[0][1], w[1][0],
+                                                               w[1][1], G)] for w in gu]
+        def unfused_step(w):
+            h = mmfp4.marlin_gemm_fp4(a, w[0], w[1], G)
+            return torch.nn.functional.silu(h[:, :N]) * h[:, N:]
+        unfused = [[lambda w=w: unfused_step(w)] for w in cat]
+        uf = 1e3 * timed_launches(torch, fused, st, 3) / st
+        uu = 1e3 * timed_launches(torch, unfused, st, 3) / st
+        byts = 2 * alg_bytes(M, K, N) - 2 * M * K
+        res[f"gate_up_silu_M{M}"] = {
+            "K": K, "N_each": N, "fused_us": round(uf, 2), "unfused_us": round(uu, 2),
+            "fused_TBps": round(byts / (uf * 1e-6) / 1e12, 3),
+            "fused_TFLOPs": round(4 * M * K * N / (uf * 1e-6) / 1e12, 1),
+            "unfused": "marlin_gemm_fp4 on the concatenated [K/8, 2N] weights + torch silu*mul"}
+    del gu, cat
+    Ns = (4096, 1024, 1024)
+    copies = max(2, -(-ROTATE_BYTES // sum(alg_bytes(0, K, n) for n in Ns)))
+    qkv = [[rand_weights(torch, K, n, gen) for n in Ns] for _ in range(copies)]
+    a = torch.randn((1, K), generator=gen, device="cuda").half()
+    fused = [[lambda w=w: mmfp4.mmfp4_fused_qkv(a, w[0][0], w[0][1], w[1][0], w[1][1], w[2][0],
+                                                w[2][1], G)] for w in qkv]
+    sep = [[lambda w=w, i=i: mmfp4.marlin_gemm_fp4(a, w[i][0], w[i][1], G) for i in range(3)]
+           for w in qkv]
+    uf = 1e3 * timed_launches(torch, fused, steps, 5) / steps
+    us = 1e3 * timed_launches(torch, sep, steps, 5) / steps
+    byts = sum(alg_bytes(1, K, n) for n in Ns) - 2 * 2 * K
+    res["qkv_M1"] = {"K": K, "N": list(Ns), "fused_us": round(uf, 2), "three_launches_us":
+                     round(us, 2), "fused_TBps": round(byts / (uf * 1e-6) / 1e12, 3)}
+    return res
+
+
+def hipblaslt_fp16_reference(torch, M: int):
+    """Plain fp16 GEMM (torch.matmul -> hipBLASLt) on the prefill shapes with
+    already-dequantised weights: the vendor library's rate for the same
+    arithmetic without the FP4 decode, as context for the prefill figure."""
+    out = {}
+    for name, K, N in PREFILL:
+        a = torch.randn((M, K), device="cuda").half()
+        w = torch.randn((K, N), device="cuda").half()
+        for _ in range(3):
+            a @ w
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(10):
+            a @ w
+        t1.record()
+        torch.cuda.synchronize()
+        us = 1e3 * t0.elapsed_time(t1) / 10
+        out[name] = {"us": round(us, 2), "TFLOPs": round(2 * M * K * N / (us * 1e-6) / 1e12, 1)}
+    return out
+
+
 MOE = {"E": 128, "H": 2048, "I": 768, "k": 8}
 
 
@@ -355,6 +429,8 @@ def main() -> int:
     }
     out["config1_single_linear_m1"] = run_single_bench(torch, mmfp4, 1, 4096, 4096, 100)
     out["config5_moe_qwen3_30b_a3b"] = [run_moe_bench(torch, mmfp4, T, 20) for T in (32, 1024)]
+    out["prefill_m2048"]["hipblaslt_fp16_same_shapes"] = hipblaslt_fp16_reference(torch, 2048)
+    out["fused_next_rows"] = run_fused_bench(torch, mmfp4, 100)
     if args.all:
         extra = {}
         for M in (8, 32):
