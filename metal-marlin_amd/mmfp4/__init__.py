@@ -11,7 +11,9 @@ from .kernels import (FP4_PER_UINT, decode_gemv_fp4, dequant_fp4, dequant_fp4_de
 from .moe_dispatch import (MoEDispatcher, MoEDispatchInfo, compute_expert_load,
                            compute_load_balancing_loss, gather_for_experts,
                            group_tokens_by_expert, group_tokens_by_expert_full,
-                           moe_expert_gemm_fp4, moe_mlp_fp4, moe_router_topk,
+                           fused_router_topk, mmfp4_softmax_topk, moe_expert_gemm_fp4,
+                           moe_fused_router_sorted, moe_mlp_fp4, moe_router_topk,
+                           router_softmax_topk,
                            scatter_expert_outputs)
 from .quantize_fp4 import (E2M1_VALUES, compute_quantization_error, pack_u4_weights,
                            quantize_fp4, unpack_fp4, unpack_u4_weights)

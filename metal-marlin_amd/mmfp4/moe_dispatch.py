@@ -108,12 +108,83 @@ def compute_load_balancing_loss(expert_probs_pre_topk: torch.Tensor, expert_ids:
     return num_experts * (f * expert_probs_pre_topk.mean(dim=0)).sum()
 
 
+def _router(hidden: torch.Tensor, weight_eh: torch.Tensor, bias: torch.Tensor | None,
+            top_k: int, renormalize: bool):
+    """One launch: logits = hidden @ weight_eh^T (+ bias), rounded to fp16 as
+    the gate's fp16 output is, then fp32 softmax -> top-k -> optional
+    renormalisation.  Returns (probs fp32 [T, k], ids int64 [T, k])."""
+    dev = _lib.require_device(hidden, weight_eh, bias)
+    H = hidden.shape[-1]
+    x = _half(hidden.reshape(-1, H))
+    w = _half(weight_eh)
+    if w.dim() != 2 or w.shape[1] != H:
+        raise ValueError(f"router weight must be [num_experts, {H}], got {tuple(w.shape)}")
+    T, E = x.shape[0], w.shape[0]
+    b = None if bias is None else bias.to(torch.float32).contiguous()
+    ids = torch.empty((T, top_k), dtype=torch.int64, device=dev)
+    probs = torch.empty((T, top_k), dtype=torch.float32, device=dev)
+    _lib.call("mm_moe_router", _lib.ptr(x), _lib.ptr(w), _lib.ptr(b), T, H, E, top_k,
+              int(renormalize), _lib.ptr(ids), _lib.ptr(probs), _lib.stream_of(x))
+    return probs, ids
+
+
 def moe_router_topk(hidden: torch.Tensor, router_weights: torch.Tensor, top_k: int = 2):
     """softmax(hidden @ router_weights) -> top-k -> renormalise
-    (kernels/moe.py:729-740).  Returns (ids, probs)."""
-    probs = torch.softmax(torch.matmul(hidden, router_weights).to(torch.float32), dim=-1)
-    topk_probs, topk_ids = torch.topk(probs, k=top_k, dim=-1)
-    return topk_ids, topk_probs / topk_probs.sum(dim=-1, keepdim=True)
+    (kernels/moe.py:729-740), router_weights [H, E], in one launch.
+    Returns (ids int64, probs fp32)."""
+    probs, ids = _router(hidden, router_weights.t(), None, top_k, True)
+    return ids, probs
+
+
+def fused_router_topk(hidden_states: torch.Tensor, gate: nn.Linear, top_k: int,
+                      training: bool = False, use_metal: bool = True):
+    """Router GEMV + softmax + top-k + renormalise in one launch
+    (moe_dispatch.py:178-219, _fused_router_topk; the math of its torch path,
+    gate(hidden) -> _router_softmax_fusion(renormalize=True)).  gate.weight is
+    [num_experts, hidden]; returns (topk_weights in the gate's dtype,
+    topk_indices int64).  `training` and `use_metal` are accepted for
+    signature parity; there is one implementation."""
+    probs, ids = _router(hidden_states, gate.weight.detach(),
+                         None if gate.bias is None else gate.bias.detach(), top_k, True)
+    return probs.to(gate.weight.dtype), ids
+
+
+def router_softmax_topk(gate_logits: torch.Tensor, top_k: int, renormalize: bool = True):
+    """fp32 softmax -> top-k (descending) -> optional renormalisation of given
+    logits [T, E] in one launch (moe_dispatch.py:99-151,
+    _router_softmax_fusion).  Returns (topk_probs in the logits' dtype,
+    topk_indices int64)."""
+    dev = _lib.require_device(gate_logits)
+    E = gate_logits.shape[-1]
+    lg = gate_logits.reshape(-1, E)
+    f32 = lg.dtype != torch.float16
+    lg = (lg.to(torch.float32) if f32 else lg).contiguous()
+    T = lg.shape[0]
+    ids = torch.empty((T, top_k), dtype=torch.int64, device=dev)
+    probs = torch.empty((T, top_k), dtype=torch.float32, device=dev)
+    _lib.call("mm_softmax_topk", _lib.ptr(lg), int(f32), T, E, top_k, int(renormalize),
+              _lib.ptr(ids), _lib.ptr(probs), _lib.stream_of(lg))
+    lead = tuple(gate_logits.shape[:-1])
+    return probs.to(gate_logits.dtype).reshape(*lead, top_k), ids.reshape(*lead, top_k)
+
+
+def mmfp4_softmax_topk(logits: torch.Tensor, top_k: int = 4):
+    """Softmax over the experts then top-k, no renormalisation
+    (kernels_core.py:241-247 -> the mmfp4_softmax_topk kernel :966):
+    logits [B, E] -> (probs fp16 [B, k], indices int64 [B, k])."""
+    probs, ids = router_softmax_topk(logits, top_k, renormalize=False)
+    return probs.to(torch.float16), ids
+
+
+def moe_fused_router_sorted(hidden_states: torch.Tensor, gate: nn.Linear, top_k: int):
+    """Router -> softmax -> top-k -> renormalise, then the stable expert sort:
+    two launches and no host synchronisation (moe_dispatch.py:328-449,
+    _fused_router_topk_metal with the moe_fused_router_sorted kernel, whose
+    grouping is not stable; this one is).  Returns (topk_weights, topk_ids,
+    MoEDispatchInfo)."""
+    w, ids = fused_router_topk(hidden_states, gate, top_k)
+    info = group_tokens_by_expert_full(ids, gate.weight.shape[0])
+    return w, ids, info
 
 
 def _grouped(x, sorted_idx, offsets, gather: bool, k: int, T: int, packed, scales,
@@ -197,8 +268,8 @@ class MoEDispatcher(nn.Module):
             raise ValueError("gate_logits must be [tokens, num_experts]")
         if gate_logits.shape[0] != flat.shape[0]:
             raise ValueError("gate_logits batch must match hidden tokens")
-        probs = gate_logits.softmax(dim=-1)
-        topk_w, topk_i = torch.topk(probs, k=self.num_experts_per_tok, dim=-1)
+        topk_w, topk_i = router_softmax_topk(gate_logits, self.num_experts_per_tok,
+                                             renormalize=False)
         info = group_tokens_by_expert_full(topk_i, self.num_experts)
         xin = gather_for_experts(flat, info)
         out_dim = getattr(self.experts[0], "out_features", flat.shape[-1])
