@@ -206,6 +206,21 @@ def run_fused_bench(torch, mmfp4, steps: int):
     byts = sum(alg_bytes(1, K, n) for n in Ns) - 2 * 2 * K
     res["qkv_M1"] = {"K": K, "N": list(Ns), "fused_us": round(uf, 2), "three_launches_us":
                      round(us, 2), "fused_TBps": round(byts / (uf * 1e-6) / 1e12, 3)}
+    # Router (config 5 shape): gate GEMM + softmax + top-8 + renormalise.
+    E, H, k = MOE["E"], MOE["H"], MOE["k"]
+    gate = torch.nn.Linear(H, E, bias=False).to("cuda").half()
+    for T in (32, 1024):
+        x = torch.randn((T, H), generator=gen, device="cuda").half()
+
+        def torch_router():
+            p = torch.softmax(gate(x).float(), -1)
+            w, i = torch.topk(p, k, -1)
+            return (w / w.sum(-1, keepdim=True)).half(), i
+        uf = 1e3 * timed_launches(torch, [[lambda: mmfp4.fused_router_topk(x, gate, k)]],
+                                  steps, 5) / steps
+        ut = 1e3 * timed_launches(torch, [[torch_router]], steps, 5) / steps
+        res[f"router_T{T}"] = {"E": E, "H": H, "k": k, "fused_us": round(uf, 2),
+                               "torch_ops_us": round(ut, 2)}
     return res
 
 
