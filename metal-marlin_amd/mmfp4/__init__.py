@@ -8,6 +8,7 @@ from .kernels import (FP4_PER_UINT, decode_gemv_fp4, dequant_fp4, dequant_fp4_de
                       marlin_gemm_int4, mmfp4_fused_gate_up, mmfp4_fused_gate_up_marlin,
                       mmfp4_fused_qkv,
                       mmfp4_gemm, select_decode_kernel)
+from .layers import MMFP4Linear
 from .loader import QuantizedModel, convert_safetensors_to_fp4, load_and_quantize_safetensors
 from .moe_dispatch import (MoEDispatcher, MoEDispatchInfo, compute_expert_load,
                            compute_load_balancing_loss, gather_for_experts,
