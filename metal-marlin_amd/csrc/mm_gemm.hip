@@ -427,7 +427,8 @@ k_prefill2(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
   // columns and tile 1 the same 32 up columns, so a block covers BN/2 output
   // columns.  Requires K % 64 == 0 and N % 8 == 0 (checked by the host).
   static_assert(ACT == SK_PLAIN || CW == 2, "pair modes pair two column tiles");
-  using Sh = Pf2Shape<INT4, WM, WN, RB, CW>;
+  constexpr int SROWS = G64 ? PF2_SROWS_G64 : PF2_SROWS;
+  using Sh = Pf2Shape<INT4, WM, WN, RB, CW, PF2_STAGES, SROWS>;
   __shared__ __attribute__((aligned(16))) char smem[Sh::LDS_BYTES];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / WN, wn = wave % WN;
@@ -443,10 +444,12 @@ k_prefill2(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
   f32x16 acc[RB][CW];
   if constexpr (ACT == SK_PLAIN) {
     const DenseSrc src{A, lda, M, m0, N, n0, B, S, Z, N};
-    pf2_mainloop<INT4, WM, WN, RB, CW, G64, false>(src, K, g, c_beg, c_end, RB, smem, acc);
+    pf2_mainloop<INT4, WM, WN, RB, CW, G64, false, PF2_STAGES, SROWS>(src, K, g, c_beg, c_end, RB,
+                                                                   smem, acc);
   } else {
     const PairSrc src{A, lda, M, m0, N, n0, B, B2, S, S2, Z, Z2, N};
-    pf2_mainloop<INT4, WM, WN, RB, CW, G64, true>(src, K, g, c_beg, c_end, RB, smem, acc);
+    pf2_mainloop<INT4, WM, WN, RB, CW, G64, true, PF2_STAGES, SROWS>(src, K, g, c_beg, c_end, RB,
+                                                                  smem, acc);
   }
 
   typedef f16 svec __attribute__((ext_vector_type(CW)));

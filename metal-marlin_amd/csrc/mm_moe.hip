@@ -18,6 +18,9 @@ namespace {
 using namespace mmsk;
 using namespace mmpf;
 
+#ifndef MM_MOE_PF_STAGES
+#define MM_MOE_PF_STAGES 3   // LDS ring depth of the grouped prefill kernel
+#endif
 #ifndef MM_MOE_PF_ROWS
 #define MM_MOE_PF_ROWS 24   // average rows per expert above which the MFMA tile kernel runs
 #endif
@@ -267,14 +270,15 @@ struct MoeSrc {
   MM_DEV const f16* zcol(int P, int w) const { return Z + col(P, w); }
 };
 
-template <int WM, int WN, int RB, bool G64>
+template <int WM, int WN, int RB, bool G64, int STAGES>
 __global__ void __launch_bounds__(WM * WN * 64)
 k_moe_prefill(const f16* __restrict__ X, const int32_t* __restrict__ sorted_idx,
               const int32_t* __restrict__ offsets, int gather, int topk,
               const uint32_t* __restrict__ Ball, const f16* __restrict__ Sall, int E, int K,
               int N, int g, int act, int gx, f16* __restrict__ Y) {
   constexpr int CW = 2;
-  using Sh = Pf2Shape<false, WM, WN, RB, CW>;
+  constexpr int SROWS = G64 ? PF2_SROWS_G64 : PF2_SROWS;
+  using Sh = Pf2Shape<false, WM, WN, RB, CW, STAGES, SROWS>;
   constexpr int BM = Sh::BM, BN = Sh::BN;
   __shared__ __attribute__((aligned(16))) char smem[Sh::LDS_BYTES];
   __shared__ int tp[MOE_MAX_EXPERTS + 1];     // row-tile prefix over experts
@@ -327,7 +331,8 @@ k_moe_prefill(const f16* __restrict__ X, const int32_t* __restrict__ sorted_idx,
   const int rb_live =
       __builtin_amdgcn_readfirstlane(min(RB, max(0, (rows - wm * 32 * RB + 31) / 32)));
   f32x16 acc[RB][CW];
-  pf2_mainloop<false, WM, WN, RB, CW, G64, true>(src, K, g, 0, K / PF2_BK, rb_live, smem, acc);
+  pf2_mainloop<false, WM, WN, RB, CW, G64, true, STAGES, SROWS>(src, K, g, 0, K / PF2_BK, rb_live,
+                                                                smem, acc);
 
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
@@ -430,27 +435,27 @@ extern "C" int mm_moe_grouped_gemm(const uint16_t* X, const int32_t* sorted_idx,
 #else
     const int cfg = tk < 48L * E ? 1 : 3;
 #endif
-#define MM_LAUNCH_MOE_PF(WM, WN, RB)                                                           \
+#define MM_LAUNCH_MOE_PF(WM, WN, RB, ST)                                                         \
   do {                                                                                         \
     constexpr int BM = WM * 32 * RB, BN = WN * 64;                                             \
     const int gx = act ? mm_cdiv(nout, BN / 2) : mm_cdiv(N, BN);                               \
     const long blocks = (long)gx * ((tk + BM - 1) / BM + std::min<long>(E, tk));               \
     MM_CHECK_ARG(blocks < (1L << 30), "mm_moe_grouped_gemm: T*k=%ld too large", tk);           \
     if (g % PF2_BK == 0)                                                                       \
-      hipLaunchKernelGGL((k_moe_prefill<WM, WN, RB, true>), dim3((unsigned)blocks),            \
+      hipLaunchKernelGGL((k_moe_prefill<WM, WN, RB, true, ST>), dim3((unsigned)blocks), \
                          dim3(WM * WN * 64), 0, (hipStream_t)stream, (const f16*)X, sorted_idx, \
                          offsets, gather, k, B, (const f16*)S, E, K, N, g, act, gx, (f16*)Y);  \
     else                                                                                       \
-      hipLaunchKernelGGL((k_moe_prefill<WM, WN, RB, false>), dim3((unsigned)blocks),           \
+      hipLaunchKernelGGL((k_moe_prefill<WM, WN, RB, false, ST>), dim3((unsigned)blocks),\
                          dim3(WM * WN * 64), 0, (hipStream_t)stream, (const f16*)X, sorted_idx, \
                          offsets, gather, k, B, (const f16*)S, E, K, N, g, act, gx, (f16*)Y);  \
   } while (0)
     switch (cfg) {
-      case 0: MM_LAUNCH_MOE_PF(2, 4, 2); break;    // 128 x 256, 8 waves
-      case 1: MM_LAUNCH_MOE_PF(1, 4, 2); break;    // 64 x 256, 4 waves
-      case 2: MM_LAUNCH_MOE_PF(1, 8, 2); break;    // 64 x 512, 8 waves
-      case 3: MM_LAUNCH_MOE_PF(1, 4, 3); break;    // 96 x 256, 4 waves
-      default: MM_LAUNCH_MOE_PF(2, 4, 4); break;   // 256 x 256, 8 waves
+      case 0: MM_LAUNCH_MOE_PF(2, 4, 2, 3); break;                  // 128 x 256, 8 waves
+      case 1: MM_LAUNCH_MOE_PF(1, 4, 2, MM_MOE_PF_STAGES); break;   // 64 x 256, 4 waves
+      case 2: MM_LAUNCH_MOE_PF(1, 8, 2, 3); break;                  // 64 x 512, 8 waves
+      case 3: MM_LAUNCH_MOE_PF(1, 4, 3, MM_MOE_PF_STAGES); break;   // 96 x 256, 4 waves
+      default: MM_LAUNCH_MOE_PF(2, 4, 4, 3); break;                 // 256 x 256, 8 waves
     }
 #undef MM_LAUNCH_MOE_PF
     MM_CHECK_LAUNCH("mm_moe_grouped_gemm(prefill)");

@@ -3,7 +3,7 @@
 //
 // Every operand of a 64-k chunk (A tile, packed B, the scale/zero rows it
 // needs) is fetched global -> LDS directly (global_load_lds_dwordx4)
-// PF2_STAGES-1 chunks ahead, so the load latency hides behind two chunks of
+// STAGES-1 chunks ahead, so the load latency hides behind that many chunks of
 // MFMA work without staging registers.
 //   A stage: BM rows x 64 halves, 16-byte pieces XOR-swizzled by row
 //            (piece (r, c8) lives at r*8 + (c8 ^ ((r >> 1) & 7))) so the MFMA
@@ -34,14 +34,11 @@ namespace mmpf {
 using namespace mmsk;
 
 constexpr int PF2_BK = 64;
-#ifndef MM_PF2_STAGES
-#define MM_PF2_STAGES 3
-#endif
-#ifndef MM_PF2_SROWS
-#define MM_PF2_SROWS 8
-#endif
-constexpr int PF2_STAGES = MM_PF2_STAGES;   // LDS ring depth: loads run STAGES-1 chunks ahead
-constexpr int PF2_SROWS = MM_PF2_SROWS;     // scale rows staged per chunk (groups it may touch)
+constexpr int PF2_STAGES = 3;   // default LDS ring depth: loads run STAGES-1 chunks ahead
+// Scale rows staged per chunk: the groups a 64-k chunk can touch (8 for
+// g = 8); with g % 64 == 0 a chunk lies in one group and 2 rows suffice.
+constexpr int PF2_SROWS = 8;
+constexpr int PF2_SROWS_G64 = 2;
 
 template <class F, int... I>
 MM_DEV void static_for(F&& f, std::integer_sequence<int, I...>) {
@@ -62,7 +59,8 @@ MM_DEV void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((VM & 15) | (7 << 4) | (15 << 8) | ((VM >> 4) << 14));
 }
 
-template <bool INT4, int WM, int WN, int RB, int CW>
+template <bool INT4, int WM, int WN, int RB, int CW, int STAGES = PF2_STAGES,
+          int SROWS = PF2_SROWS>
 struct Pf2Shape {
   static constexpr int NTHR = WM * WN * 64;
   static constexpr int NWAVE = WM * WN;
@@ -70,7 +68,7 @@ struct Pf2Shape {
   static constexpr int BN = WN * 32 * CW;
   static constexpr int A_PIECES = BM * (PF2_BK / 8);   // 16-byte pieces per stage
   static constexpr int B_PIECES = (PF2_BK / 8) * (BN / 4);
-  static constexpr int S_PIECES = PF2_SROWS * (BN / 8);
+  static constexpr int S_PIECES = SROWS * (BN / 8);
   static_assert(A_PIECES % NTHR == 0 && B_PIECES % 64 == 0 && S_PIECES % 64 == 0, "split");
   static constexpr int A_IT = A_PIECES / NTHR;
   static constexpr int B_IT = (B_PIECES + NTHR - 1) / NTHR;
@@ -80,10 +78,10 @@ struct Pf2Shape {
   // LDS: [A stages][B stages][S stages][Z stages][dump].  Waves whose piece
   // range lies past a small operand still issue their load (vmcnt must count
   // the same loads in every thread) into the 1 KiB dump area.
-  static constexpr int B_OFF = PF2_STAGES * A_BYTES;
-  static constexpr int S_OFF = B_OFF + PF2_STAGES * B_BYTES;
-  static constexpr int Z_OFF = S_OFF + PF2_STAGES * S_BYTES;
-  static constexpr int D_OFF = Z_OFF + (INT4 ? PF2_STAGES * S_BYTES : 0);
+  static constexpr int B_OFF = STAGES * A_BYTES;
+  static constexpr int S_OFF = B_OFF + STAGES * B_BYTES;
+  static constexpr int Z_OFF = S_OFF + STAGES * S_BYTES;
+  static constexpr int D_OFF = Z_OFF + (INT4 ? STAGES * S_BYTES : 0);
   static constexpr int LDS_BYTES = D_OFF + 1024;
 };
 
@@ -97,10 +95,12 @@ struct Pf2Shape {
 //   src.ld           -> row stride of B in words and of S/Z in halves.
 // rb_live: the wave's row blocks past it hold no valid row and skip their
 // MFMAs (wave-uniform).  Requires K % 64 == 0.
-template <bool INT4, int WM, int WN, int RB, int CW, bool G64, bool TM, class Src>
+template <bool INT4, int WM, int WN, int RB, int CW, bool G64, bool TM, int STAGES, int SROWS,
+          class Src>
 MM_DEV void pf2_mainloop(const Src& src, int K, int g, int c_beg, int c_end, int rb_live,
                          char* smem, f32x16 (&acc)[RB][CW]) {
-  using Sh = Pf2Shape<INT4, WM, WN, RB, CW>;
+  static_assert(G64 || SROWS >= PF2_SROWS, "a chunk can touch 8 groups unless g % 64 == 0");
+  using Sh = Pf2Shape<INT4, WM, WN, RB, CW, STAGES, SROWS>;
   constexpr int NWAVE = Sh::NWAVE, BN = Sh::BN;
   constexpr int A_IT = Sh::A_IT, B_IT = Sh::B_IT, S_IT = Sh::S_IT;
   constexpr int A_BYTES = Sh::A_BYTES, B_BYTES = Sh::B_BYTES, S_BYTES = Sh::S_BYTES;
@@ -168,7 +168,7 @@ MM_DEV void pf2_mainloop(const Src& src, int K, int g, int c_beg, int c_end, int
       for (int v = 0; v < 16; ++v) acc[rb][j][v] = 0.0f;
 
 #pragma unroll
-  for (int c = 0; c < PF2_STAGES - 1; ++c) issue(min(c_beg + c, nch - 1), c);
+  for (int c = 0; c < STAGES - 1; ++c) issue(min(c_beg + c, nch - 1), c);
 
   // Per-lane LDS byte offsets, fixed for the whole K loop.
   const int colw = TM ? wn * 32 * CW + l32 : wn * 32 * CW + CW * l32;   // column of tile 0
@@ -207,9 +207,9 @@ MM_DEV void pf2_mainloop(const Src& src, int K, int g, int c_beg, int c_end, int
     // Chunk ch's loads are complete once at most (STAGES-2) later chunks' loads
     // are outstanding; the barrier then publishes every thread's pieces and
     // guarantees the stage refilled below has been consumed by all waves.
-    wait_vmcnt<(PF2_STAGES - 2) * Sh::LOADS_PER_CHUNK>();
+    wait_vmcnt<(STAGES - 2) * Sh::LOADS_PER_CHUNK>();
     __builtin_amdgcn_s_barrier();
-    issue(min(ch + PF2_STAGES - 1, nch - 1), (st + PF2_STAGES - 1) % PF2_STAGES);
+    issue(min(ch + STAGES - 1, nch - 1), (st + STAGES - 1) % STAGES);
     const int k0 = ch * PF2_BK;
     const int gi0 = k0 / g;
     f16x8 af[2][RB];
@@ -283,13 +283,13 @@ MM_DEV void pf2_mainloop(const Src& src, int K, int g, int c_beg, int c_end, int
   };
   // The ring position of chunk ch is (ch - c_beg) % STAGES: unroll by STAGES so
   // every LDS offset is a compile-time constant.
-  for (int ch = c_beg; ch < nch; ch += PF2_STAGES) {
+  for (int ch = c_beg; ch < nch; ch += STAGES) {
     static_for(
         [&](auto stc) {
           constexpr int st = decltype(stc)::value;
           if (st == 0 || ch + st < nch) chunk(ch + st, stc);
         },
-        std::make_integer_sequence<int, PF2_STAGES>{});
+        std::make_integer_sequence<int, STAGES>{});
   }
   wait_vmcnt<0>();
 }

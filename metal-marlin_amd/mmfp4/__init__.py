@@ -9,6 +9,7 @@ from .kernels import (FP4_PER_UINT, decode_gemv_fp4, dequant_fp4, dequant_fp4_de
                       mmfp4_fused_qkv,
                       mmfp4_gemm, select_decode_kernel)
 from .layers import MMFP4Linear
+from .ops import GemmFp4, dispatch_gemm_fp4
 from .loader import QuantizedModel, convert_safetensors_to_fp4, load_and_quantize_safetensors
 from .moe_dispatch import (MoEDispatcher, MoEDispatchInfo, compute_expert_load,
                            compute_load_balancing_loss, gather_for_experts,

@@ -51,3 +51,20 @@ def test_mmfp4_linear_errors():
                               None, 32)
     with pytest.raises(ValueError, match="Expected input last dim"):
         layer(torch.zeros((1, 32), dtype=torch.float16, device="cuda"))
+
+
+def test_dispatch_gemm_fp4_and_gemmfp4(rng):
+    """metal_dispatch.dispatch_gemm_fp4 / ops.GemmFp4 signatures over the same
+    kernels, against the oracle; `out=` is filled in place."""
+    import mmfp4
+    M, K, N, g = 7, 256, 96, 32
+    w = rng.normal(0, 0.02, (N, K)).astype(np.float16)
+    p, s = ofp4.quantize_fp4(w, g)
+    x = rng.normal(0, 1, (M, K)).astype(np.float16)
+    ref = ofp4.gemm_fp4_ref(x, p, s, g)
+    announce("dispatch_gemm_fp4 / GemmFp4")
+    out = torch.empty((M, N), dtype=torch.float16, device="cuda")
+    r = mmfp4.dispatch_gemm_fp4(None, to_dev(x), to_dev(p), to_dev(s), M, N, K, g, out=out)
+    assert r is out and max_abs_rel(to_np(out), ref) <= TOL
+    y = mmfp4.GemmFp4()(to_dev(x[None]), to_dev(p), to_dev(s), g)
+    assert tuple(y.shape) == (1, M, N) and max_abs_rel(to_np(y[0]), ref) <= TOL
