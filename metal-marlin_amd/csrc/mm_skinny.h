@@ -10,9 +10,10 @@
 //
 // Group scales: when the group size is a multiple of 32 (FL > 0) a group
 // covers whole steps and the same group for every lane, so the MFMAs of a
-// group accumulate unscaled E2M1 values (or q - z for INT4) and the group
-// sum is multiplied by the fp32 scale once ("post-scale"); the per-word decode
-// is then four packed converts.  Other group sizes (FL == 0) scale every
+// group accumulate unscaled E2M1 values and the group sum is multiplied by
+// the fp32 scale once ("post-scale"); the per-word decode is then four packed
+// converts.  INT4 groups accumulate a * (1024 + q) and subtract
+// (1024 + z) * sum(a) (u4_magic_word below).  Other group sizes (FL == 0) scale every
 // word in fp16 before the MFMA (the reference's rounding of each weight).
 #pragma once
 #include "mm_common.h"
@@ -35,19 +36,39 @@ struct WordDq<true> {
   }
 };
 
-// Unscaled word decode: E2M1 values, or fp16(q - z) for INT4.
+// Unscaled FP4 word decode: the E2M1 values.
 MM_DEV f16x8 raw_fp4_word(uint32_t w) {
   const f16x2 p0 = e2m1_pair_c<0>(w), p1 = e2m1_pair_c<1>(w);
   const f16x2 p2 = e2m1_pair_c<2>(w), p3 = e2m1_pair_c<3>(w);
   return f16x8{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
 }
-MM_DEV f16x8 raw_u4_word(uint32_t w, f16x2 negz2) {
-  const f16x2 m1024 = {(f16)-1024.0f, (f16)-1024.0f};
-  const f16x2 p0 = (u4_pair(w, 0) + m1024) + negz2;
-  const f16x2 p1 = (u4_pair(w, 8) + m1024) + negz2;
-  const f16x2 p2 = (u4_pair(w, 16) + m1024) + negz2;
-  const f16x2 p3 = (u4_pair(w, 24) + m1024) + negz2;
-  return f16x8{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+
+// INT4 post-scale decode.  Word w holds codes q0..q7 (nibble i = k row i).
+// Each packed half is the fp16 number 1024 + q (exponent 10, q in the low
+// mantissa bits), paired as (q0, q4), (q1, q5), (q2, q6), (q3, q7): one
+// and-or per pair after a shift.  The MFMA then sums a * (1024 + q) exactly
+// (11-bit by 11-bit products) and the group epilogue subtracts
+// (1024 + z) * sum(a), with sum(a) from one extra MFMA against a ones
+// operand.  The A operand is permuted to the same k order (a_k4_order).
+MM_DEV f16x8 u4_magic_word(uint32_t w) {
+  u32x4 p;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) p[i] = ((w >> (4 * i)) & 0x000F000Fu) | 0x64006400u;
+  return __builtin_bit_cast(f16x8, p);
+}
+// (a0..a7) -> (a0, a4, a1, a5, a2, a6, a3, a7): the k order of u4_magic_word.
+MM_DEV f16x8 a_k4_order(f16x8 a) {
+  const u32x4 d = __builtin_bit_cast(u32x4, a);
+  u32x4 o;
+  o[0] = __builtin_amdgcn_perm(d[2], d[0], 0x05040100u);
+  o[1] = __builtin_amdgcn_perm(d[2], d[0], 0x07060302u);
+  o[2] = __builtin_amdgcn_perm(d[3], d[1], 0x05040100u);
+  o[3] = __builtin_amdgcn_perm(d[3], d[1], 0x07060302u);
+  return __builtin_bit_cast(f16x8, o);
+}
+MM_DEV f16x8 f16x8_ones() {
+  const f16 o = (f16)1.0f;
+  return f16x8{o, o, o, o, o, o, o, o};
 }
 
 template <typename T>
@@ -156,23 +177,29 @@ MM_DEV void skinny_wave(const f16* __restrict__ A, int lda, const int* __restric
           if constexpr (INT4) z4[t] = *at_bytes<f16x4>(tl[t].Z, (gi * (uint32_t)N + coff[t]) * 2u);
         }
         f32x4 grp[MT][NT][4];
+        f32x4 asum[MT];                     // INT4: sum of A over the group, per row
 #pragma unroll
         for (int i = f * FL; i < (f + 1) * FL; ++i) {
+          f16x8 ai[MT];
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            if constexpr (INT4) {
+              asum[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                  a[i][mt], f16x8_ones(), i == f * FL ? f32x4{0, 0, 0, 0} : asum[mt], 0, 0, 0);
+              ai[mt] = a_k4_order(a[i][mt]);
+            } else {
+              ai[mt] = a[i][mt];
+            }
+          }
 #pragma unroll
           for (int t = 0; t < NT; ++t) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-              f16x8 b;
-              if constexpr (INT4) {
-                const f16 nz = -clamp_zero(z4[t][j]);
-                b = raw_u4_word(w[i][t][j], f16x2{nz, nz});
-              } else {
-                b = raw_fp4_word(w[i][t][j]);
-              }
+              const f16x8 b = INT4 ? u4_magic_word(w[i][t][j]) : raw_fp4_word(w[i][t][j]);
 #pragma unroll
               for (int mt = 0; mt < MT; ++mt)
                 grp[mt][t][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                    a[i][mt], b, i == f * FL ? f32x4{0, 0, 0, 0} : grp[mt][t][j], 0, 0, 0);
+                    ai[mt], b, i == f * FL ? f32x4{0, 0, 0, 0} : grp[mt][t][j], 0, 0, 0);
             }
           }
         }
@@ -181,8 +208,15 @@ MM_DEV void skinny_wave(const f16* __restrict__ A, int lda, const int* __restric
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             const float sc = (float)sanitize_scale(s4[t][j]);
+            if constexpr (INT4) {
+              const float zb = 1024.0f + (float)clamp_zero(z4[t][j]);
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt) acc[mt][t][j] += sc * grp[mt][t][j];
+              for (int mt = 0; mt < MT; ++mt)
+                acc[mt][t][j] += sc * (grp[mt][t][j] - zb * asum[mt]);
+            } else {
+#pragma unroll
+              for (int mt = 0; mt < MT; ++mt) acc[mt][t][j] += sc * grp[mt][t][j];
+            }
           }
       }
     }
@@ -280,34 +314,38 @@ MM_DEV void strip_wave(const f16* __restrict__ A, int lda, const int* __restrict
     for (int f = 0; f < SPW / FL; ++f) {
       const int slg = min(slb + f * FL, nsl - 1);
       const uint32_t gi = (uint32_t)((slg * 32) / g);
-      f16x4 s4[NS];
-      f16 zc[NS];
+      f16x4 s4[NS], z4[NS];
 #pragma unroll
       for (int t = 0; t < NS; ++t) {
         s4[t] = *at_bytes<f16x4>(S, (gi * (uint32_t)N + scol[t]) * 2u);
-        if constexpr (INT4) zc[t] = *at_bytes<f16>(Z, (gi * (uint32_t)N + bcol[t]) * 2u);
+        if constexpr (INT4) z4[t] = *at_bytes<f16x4>(Z, (gi * (uint32_t)N + scol[t]) * 2u);
       }
-      f32x4 grp[NS];
+      // INT4: weights decode to 1024 + q (u4_magic_word); asum (every row)
+      // is the activation row's sum over the group.
+      f32x4 grp[NS], asum;
 #pragma unroll
       for (int u = f * FL; u < (f + 1) * FL; ++u) {
+        f16x8 au = R.a[u];
+        if constexpr (INT4) {
+          asum = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+              f16x8_ones(), au, u == f * FL ? f32x4{0, 0, 0, 0} : asum, 0, 0, 0);
+          au = a_k4_order(au);
+        }
 #pragma unroll
         for (int t = 0; t < NS; ++t) {
-          f16x8 b;
-          if constexpr (INT4) {
-            const f16 nz = -clamp_zero(zc[t]);
-            b = raw_u4_word(R.w[u][t], f16x2{nz, nz});
-          } else {
-            b = raw_fp4_word(R.w[u][t]);
-          }
+          const f16x8 b = INT4 ? u4_magic_word(R.w[u][t]) : raw_fp4_word(R.w[u][t]);
           grp[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-              b, R.a[u], u == f * FL ? f32x4{0, 0, 0, 0} : grp[t], 0, 0, 0);
+              b, au, u == f * FL ? f32x4{0, 0, 0, 0} : grp[t], 0, 0, 0);
         }
       }
 #pragma unroll
       for (int t = 0; t < NS; ++t)
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr)
-          acc[t][rr] += (float)sanitize_scale(s4[t][rr]) * grp[t][rr];
+        for (int rr = 0; rr < 4; ++rr) {
+          float v = grp[t][rr];
+          if constexpr (INT4) v -= (1024.0f + (float)clamp_zero(z4[t][rr])) * asum[rr];
+          acc[t][rr] += (float)sanitize_scale(s4[t][rr]) * v;
+        }
     }
   };
   // Rounds whose first slab is past the end are skipped (wave-uniform).
