@@ -746,17 +746,20 @@ int gemm_dispatch(const char* who, const f16* A, const uint32_t* B, const f16* S
                    ((uintptr_t)C & 7) == 0 && (!INT4 || ((uintptr_t)Z & 7) == 0),
                "%s: operands must be 16-byte (A, B) / 8-byte (scales, zeros, C) aligned", who);
   if (M == 0) return 0;
-  if (MM_ST_MODE && M <= 16 && flush_steps(g, MM_ST_SPW) > 0) {
+  // The decode kernels address one weight matrix with 32-bit byte offsets;
+  // larger matrices take the prefill kernels (64-bit addressing) at any M.
+  const bool off32 = (size_t)(K / 8) * (size_t)N * 4 < ((size_t)1 << 32);
+  if (off32 && MM_ST_MODE && M <= 16 && flush_steps(g, MM_ST_SPW) > 0) {
     // Column strips (no split-K hand-off) win for small layers, where the
     // hand-off is a large share of the launch; split-K wins from ~13 MB up
     // (measured on MI355X: 4096x4096 5.8 vs 7.0 us, 4096x6144 8.0 vs 7.2 us).
     if (MM_ST_MODE == 2 || ((long)K * N <= 4096L * 4096 && N / 16 >= 128))
       return launch_strip<INT4, 1>(A, K, B, S, Z, C, N, M, N, K, g, st);
   }
-  if (M <= 16)
+  if (off32 && M <= 16)
     return launch_skinny<INT4, 1, SK_PLAIN>(A, K, B, S, Z, nullptr, nullptr, nullptr, C, N, M, N,
                                             K, g, ws, ws_bytes, st);
-  if (M <= 32)
+  if (off32 && M <= 32)
     return launch_skinny<INT4, 2, SK_PLAIN>(A, K, B, S, Z, nullptr, nullptr, nullptr, C, N, M, N,
                                             K, g, ws, ws_bytes, st);
   // The pipelined kernel stages scale rows in 8-column pieces (N % 8 == 0)
@@ -814,10 +817,13 @@ int pair_dispatch(const char* who, const f16* A, const uint32_t* Bg, const f16* 
                "%s: A, packed weights, scales and zeros must be 16-byte aligned, C 8-byte", who);
   if (M == 0) return 0;
   const int ldc = ACT == SK_SWIGLU ? N : 2 * N;
-  if (M <= 16)
+  const bool off32 = (size_t)(K / 8) * (size_t)N * 4 < ((size_t)1 << 32);
+  MM_CHECK_ARG(off32 || K % PF2_BK == 0, "%s: weights over 4 GiB need K %% %d == 0", who,
+               PF2_BK);
+  if (off32 && M <= 16)
     return launch_skinny<INT4, 1, ACT>(A, K, Bg, Sg, Zg, Bu, Su, Zu, C, ldc, M, N, K, g, ws,
                                        ws_bytes, st);
-  if (M <= 32)
+  if (off32 && M <= 32)
     return launch_skinny<INT4, 2, ACT>(A, K, Bg, Sg, Zg, Bu, Su, Zu, C, ldc, M, N, K, g, ws,
                                        ws_bytes, st);
   const PrefillPlan p = plan_prefill(M, 2 * N, K);
@@ -869,7 +875,11 @@ int multi_dispatch(const char* who, const f16* A, int nmat, const uint32_t* cons
   for (int p = nmat; p < 3; ++p) mp.tile0[p] = tiles;
   mp.tile0[3] = tiles;
   mp.ntot = ntot;
-  if (M > 16 || flush_steps(g, sk_spw<1>()) == 0 || K % 8 != 0 || g <= 0 || K % g != 0) {
+  bool off32 = true;
+  for (int p = 0; p < nmat; ++p)
+    off32 = off32 && (size_t)(K / 8) * (size_t)N[p] * 4 < ((size_t)1 << 32);
+  if (!off32 || M > 16 || flush_steps(g, sk_spw<1>()) == 0 || K % 8 != 0 || g <= 0 ||
+      K % g != 0) {
     // One product per launch (M > 16, or shapes the GEMM entry rejects with
     // its own message).
     for (int p = 0; p < nmat; ++p) {

@@ -18,6 +18,12 @@ namespace {
 using namespace mmsk;
 using namespace mmpf;
 
+#ifndef MM_MOE_DEC_NW
+#define MM_MOE_DEC_NW 4      // waves per block of the grouped decode kernel (busy launches)
+#endif
+#ifndef MM_MOE_DEC_SPW
+#define MM_MOE_DEC_SPW 4     // 32-k steps per wave per round there
+#endif
 #ifndef MM_MOE_PF_STAGES
 #define MM_MOE_PF_STAGES 3   // LDS ring depth of the grouped prefill kernel
 #endif
@@ -420,6 +426,8 @@ extern "C" int mm_moe_grouped_gemm(const uint16_t* X, const int32_t* sorted_idx,
   MM_CHECK_ARG(act ? (N % 8 == 0) : (N % 4 == 0),
                "mm_moe_grouped_gemm: N=%d must be divisible by %d", N, act ? 8 : 4);
   if (T == 0) return 0;
+  MM_CHECK_ARG((size_t)(K / 8) * (size_t)N * 4 < ((size_t)1 << 32),
+               "mm_moe_grouped_gemm: one expert's packed weights must be under 4 GiB");
   const int nout = act ? N / 2 : N;
   // Prefill-sized groups (more than MM_MOE_PF_ROWS rows per expert on
   // average) run the MFMA tile kernel when the shapes allow its 16-byte
@@ -488,7 +496,7 @@ extern "C" int mm_moe_grouped_gemm(const uint16_t* X, const int32_t* sorted_idx,
   if (cfg == 0) {
     MM_LAUNCH_MOE_FL(1, 8, 8);
   } else {
-    MM_LAUNCH_MOE_FL(1, 4, 4);
+    MM_LAUNCH_MOE_FL(1, MM_MOE_DEC_NW, MM_MOE_DEC_SPW);
   }
 #undef MM_LAUNCH_MOE_FL
 #undef MM_LAUNCH_MOE
