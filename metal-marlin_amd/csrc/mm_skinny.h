@@ -113,12 +113,30 @@ MM_DEV void skinny_wave(const f16* __restrict__ A, int lda, const int* __restric
 #pragma unroll
   for (int t = 0; t < NT; ++t) coff[t] = (uint32_t)min(tl[t].col0 + 4 * c, N - 4);
 
+  st0 = __builtin_amdgcn_readfirstlane(st0);   // wave-uniform: group indices stay scalar
+  constexpr int NF = FL > 0 ? SPW / FL : 1;    // scale groups per round (post-scale)
   for (int r = 0; r < nrounds; ++r) {
     const int stb = st0 + r * ststride;    // wave-uniform
     if (stb >= nsteps) break;
     u32x4 w[SPW][NT];
     f16x8 a[SPW][MT];
-    // Issue every weight/activation load of the round before any math.
+    f16x4 s4[NF][NT], z4[NF][NT];
+    // Issue every load of the round before any math: the (small) scale and
+    // zero rows first, so that waiting for a step's weights never waits
+    // behind a scale load issued later.
+    if constexpr (FL > 0) {
+#pragma unroll
+      for (int f = 0; f < NF; ++f) {
+        const int stg = min(stb + f * FL, nsteps - 1);
+        const uint32_t gi = (uint32_t)((stg * 32) / g);      // scalar
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          s4[f][t] = *at_bytes<f16x4>(tl[t].S, (gi * (uint32_t)N + coff[t]) * 2u);
+          if constexpr (INT4)
+            z4[f][t] = *at_bytes<f16x4>(tl[t].Z, (gi * (uint32_t)N + coff[t]) * 2u);
+        }
+      }
+    }
 #pragma unroll
     for (int i = 0; i < SPW; ++i) {
       const int kp = min(4 * min(stb + i, nsteps - 1) + q, KP - 1);
@@ -167,15 +185,7 @@ MM_DEV void skinny_wave(const f16* __restrict__ A, int lda, const int* __restric
     } else {
       // Post-scale: one group per FL steps, uniform across the wave.
 #pragma unroll
-      for (int f = 0; f < SPW / FL; ++f) {
-        const int stg = min(stb + f * FL, nsteps - 1);
-        const uint32_t gi = (uint32_t)((stg * 32) / g);      // scalar
-        f16x4 s4[NT], z4[NT];
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-          s4[t] = *at_bytes<f16x4>(tl[t].S, (gi * (uint32_t)N + coff[t]) * 2u);
-          if constexpr (INT4) z4[t] = *at_bytes<f16x4>(tl[t].Z, (gi * (uint32_t)N + coff[t]) * 2u);
-        }
+      for (int f = 0; f < NF; ++f) {
         f32x4 grp[MT][NT][4];
         f32x4 asum[MT];                     // INT4: sum of A over the group, per row
 #pragma unroll
@@ -207,9 +217,9 @@ MM_DEV void skinny_wave(const f16* __restrict__ A, int lda, const int* __restric
         for (int t = 0; t < NT; ++t)
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            const float sc = (float)sanitize_scale(s4[t][j]);
+            const float sc = (float)sanitize_scale(s4[f][t][j]);
             if constexpr (INT4) {
-              const float zb = 1024.0f + (float)clamp_zero(z4[t][j]);
+              const float zb = 1024.0f + (float)clamp_zero(z4[f][t][j]);
 #pragma unroll
               for (int mt = 0; mt < MT; ++mt)
                 acc[mt][t][j] += sc * (grp[mt][t][j] - zb * asum[mt]);
@@ -267,10 +277,11 @@ MM_DEV void skinny_block_reduce(float* red, f32x4 (&acc)[MT][NT][4]) {
 // Wave w takes slabs w*SPW + r*slstride + u.  Rounds are software-pipelined:
 // round r+1's loads are issued before round r's math.
 // ---------------------------------------------------------------------------
-template <int NS, int SPW>
+template <int NS, int SPW, int NF>
 struct StripRound {
   uint32_t w[SPW][NS];
   f16x8 a[SPW];
+  f16x4 s[NF][NS], z[NF][NS];   // scale (and INT4 zero) rows of the round's groups
 };
 
 template <bool INT4, int NS, int SPW, int FL>
@@ -292,8 +303,22 @@ MM_DEV void strip_wave(const f16* __restrict__ A, int lda, const int* __restrict
     bcol[t] = (uint32_t)min(n0 + 16 * t + i, N - 1);           // weight column
     scol[t] = (uint32_t)min(n0 + 16 * t + 4 * kb, N - 4);      // output columns
   }
-  auto load = [&](int r, StripRound<NS, SPW>& R) {
+  constexpr int NF = SPW / FL;
+  sl0 = __builtin_amdgcn_readfirstlane(sl0);   // wave-uniform: group indices stay scalar
+  // Scales first: a wait for a slab's weights then never waits behind a
+  // scale load issued after them.
+  auto load = [&](int r, StripRound<NS, SPW, NF>& R) {
     const int slb = sl0 + r * slstride;
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+      const int slg = min(slb + f * FL, nsl - 1);
+      const uint32_t gi = (uint32_t)((slg * 32) / g);
+#pragma unroll
+      for (int t = 0; t < NS; ++t) {
+        R.s[f][t] = *at_bytes<f16x4>(S, (gi * (uint32_t)N + scol[t]) * 2u);
+        if constexpr (INT4) R.z[f][t] = *at_bytes<f16x4>(Z, (gi * (uint32_t)N + scol[t]) * 2u);
+      }
+    }
 #pragma unroll
     for (int u = 0; u < SPW; ++u) {
       const int kp = min(4 * min(slb + u, nsl - 1) + kb, KP - 1);
@@ -303,7 +328,7 @@ MM_DEV void strip_wave(const f16* __restrict__ A, int lda, const int* __restrict
       R.a[u] = *at_bytes<f16x8>(A, aoff + (uint32_t)kp * 16u);
     }
   };
-  auto math = [&](int r, StripRound<NS, SPW>& R) {
+  auto math = [&](int r, StripRound<NS, SPW, NF>& R) {
     const int slb = sl0 + r * slstride;
     if (slb + SPW > nsl) {
 #pragma unroll
@@ -311,15 +336,7 @@ MM_DEV void strip_wave(const f16* __restrict__ A, int lda, const int* __restrict
         if (slb + u >= nsl) R.a[u] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
     }
 #pragma unroll
-    for (int f = 0; f < SPW / FL; ++f) {
-      const int slg = min(slb + f * FL, nsl - 1);
-      const uint32_t gi = (uint32_t)((slg * 32) / g);
-      f16x4 s4[NS], z4[NS];
-#pragma unroll
-      for (int t = 0; t < NS; ++t) {
-        s4[t] = *at_bytes<f16x4>(S, (gi * (uint32_t)N + scol[t]) * 2u);
-        if constexpr (INT4) z4[t] = *at_bytes<f16x4>(Z, (gi * (uint32_t)N + scol[t]) * 2u);
-      }
+    for (int f = 0; f < NF; ++f) {
       // INT4: weights decode to 1024 + q (u4_magic_word); asum (every row)
       // is the activation row's sum over the group.
       f32x4 grp[NS], asum;
@@ -343,8 +360,8 @@ MM_DEV void strip_wave(const f16* __restrict__ A, int lda, const int* __restrict
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
           float v = grp[t][rr];
-          if constexpr (INT4) v -= (1024.0f + (float)clamp_zero(z4[t][rr])) * asum[rr];
-          acc[t][rr] += (float)sanitize_scale(s4[t][rr]) * v;
+          if constexpr (INT4) v -= (1024.0f + (float)clamp_zero(R.z[f][t][rr])) * asum[rr];
+          acc[t][rr] += (float)sanitize_scale(R.s[f][t][rr]) * v;
         }
     }
   };
@@ -352,7 +369,7 @@ MM_DEV void strip_wave(const f16* __restrict__ A, int lda, const int* __restrict
   int nr = 0;
   while (nr < nrounds && sl0 + nr * slstride < nsl) ++nr;
   if (nr == 0) return;
-  StripRound<NS, SPW> R0, R1;
+  StripRound<NS, SPW, NF> R0, R1;
   load(0, R0);
   for (int r = 0; r < nr; r += 2) {
     if (r + 1 < nr) load(r + 1, R1);

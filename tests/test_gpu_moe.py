@@ -150,3 +150,36 @@ def test_moe_prefill_config5_properties():
         y = mmfp4.marlin_gemm_fp4(a, DP[e], DS[e], g).float()
         ref.index_add_(0, tok, y * probs[tok, slot, None].float())
     assert max_abs_rel(to_np(out), to_np(ref)) <= TOL
+
+
+@pytest.mark.parametrize("T,k,E", [(5, 2, 4), (256, 8, 128), (1, 4, 64)])
+def test_gpu_grouping_api(rng, T, k, E):
+    """moe/gpu_grouping.py surface: every variant gives the oracle's stable order;
+    the manager's gather/scatter match the per-token weighted sum."""
+    import mmfp4
+    ids = rng.integers(0, E, (T, k)).astype(np.int64)
+    announce(f"gpu_grouping T={T} k={k} E={E}")
+    rs, roff, rinv = omoe.group_tokens_by_expert(ids, E)
+    d_ids = to_dev(ids)
+    E_inf = int(ids.max()) + 1
+    for res, e_want in [(mmfp4.group_tokens_by_expert_fast(d_ids, E), E),
+                        (mmfp4.group_tokens_by_expert_fast(d_ids), E_inf),
+                        (mmfp4.group_tokens_by_expert_gpu_optimized(d_ids, None, E), E),
+                        (mmfp4.group_tokens_by_expert_auto(d_ids, num_experts=E), E)]:
+        assert res.num_experts == e_want and res.num_tokens == T and res.top_k == k
+        assert res.total_assignments == T * k
+        assert np.array_equal(to_np(res.sorted_token_indices), rs // k)
+        assert np.array_equal(to_np(res.sorted_expert_indices), rs % k)
+        assert np.array_equal(to_np(res.expert_offsets)[:e_want + 1], roff[:e_want + 1])
+        assert np.array_equal(to_np(res.inverse_indices), rinv)
+    grp = mmfp4.GPUExpertGrouping(E, device="cuda")
+    res = grp.group(torch.from_numpy(ids))          # host ids are moved to the device
+    h = rng.normal(0, 1, (T, 64)).astype(np.float16)
+    xs = grp.gather_activations(to_dev(h), res)
+    assert np.array_equal(to_np(xs), h[rs // k])
+    p = rng.random((T, k)).astype(np.float32)
+    out = to_np(grp.scatter_outputs(xs, to_dev(p), res)).astype(np.float32)
+    ref = (h.astype(np.float32)[:, None, :] * p[:, :, None]).sum(1)
+    assert max_abs_rel(out, ref) <= TOL
+    with pytest.raises(ValueError):
+        mmfp4.GPUExpertGrouping(E, device="cpu")
