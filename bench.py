@@ -129,6 +129,32 @@ def run_layer_bench(torch, mmfp4, M: int, steps: int, warmup: int, int4: bool = 
             "per_shape": per_shape, "copies": copies}
 
 
+def run_read_ceiling(torch, steps: int, warmup: int):
+    """The HBM read rate this GPU reaches for the same bytes in the same
+    back-to-back launch pattern: `mm_stream_read` (a read-only stream, no
+    decode, no math) over each layer GEMM's packed weights + scales, rotated
+    copies, timed exactly like the GEMMs.  The practical ceiling of a
+    weight-streaming kernel of that size (launch, ramp-up and drain included)."""
+    from mmfp4 import _lib
+    sizes = [(name, -(-alg_bytes(0, K, N) // 16) * 16) for name, K, N in LLAMA_LAYER]
+    copies = max(2, -(-ROTATE_BYTES // sum(b for _, b in sizes)))
+    bufs = [[torch.empty(b, dtype=torch.uint8, device="cuda") for _, b in sizes]
+            for _ in range(copies)]
+    sink = torch.empty(8192 * 512, dtype=torch.int32, device="cuda")
+    st = torch.cuda.current_stream().cuda_stream
+
+    def rd(buf):
+        return lambda: _lib.call("mm_stream_read", buf.data_ptr(), buf.numel(), sink.data_ptr(),
+                                 sink.numel() * 4, st)
+    launches = [[rd(b) for b in row] for row in bufs]
+    total_ms = timed_launches(torch, launches, steps, warmup)
+    per = {name: round(us, 3) for (name, _), us in zip(sizes, per_shape_us(torch, launches))}
+    byts = sum(b for _, b in sizes)
+    return {"kernel": "mm_stream_read (16-byte non-temporal loads, no writes)",
+            "per_shape_us": per, "layer_us": round(1e3 * total_ms / steps, 3),
+            "layer_TBps": round(byts / (total_ms / steps * 1e-3) / 1e12, 3)}
+
+
 def run_prefill_bench(torch, mmfp4, M: int, steps: int, warmup: int):
     ws = [make_weights(torch, mmfp4, K, N, 7 + i) for i, (_, K, N) in enumerate(PREFILL)]
     gen = torch.Generator(device="cuda").manual_seed(2)
@@ -443,6 +469,9 @@ def main() -> int:
                           FP16_PEAK_TFLOPS, 4), "ms_per_step": round(pre["ms_per_step"], 4),
                           "per_shape": pre["per_shape"], "kernel": "k_prefill2 (MFMA 32x32x16, global->LDS pipeline)"},
     }
+    ceil = run_read_ceiling(torch, args.steps, args.warmup)
+    ceil["layer_time_fraction"] = round(ceil["layer_us"] / (1e3 * layer["ms_per_step"]), 4)
+    out["hbm_read_ceiling_m1"] = ceil
     out["config1_single_linear_m1"] = run_single_bench(torch, mmfp4, 1, 4096, 4096, 100)
     out["config5_moe_qwen3_30b_a3b"] = [run_moe_bench(torch, mmfp4, T, 20) for T in (32, 1024)]
     out["prefill_m2048"]["hipblaslt_fp16_same_shapes"] = hipblaslt_fp16_reference(torch, 2048)

@@ -161,6 +161,16 @@ int mm_moe_grouped_gemm(const uint16_t* X, const int32_t* sorted_idx, const int3
 int mm_moe_combine(const uint16_t* Y, const float* probs, const int32_t* inverse, int T, int k,
                    int H, uint16_t* out, void* stream);
 
+/* ------------------------------------------------------------ measurement */
+
+/* Reads `bytes` (a multiple of 16, 16-byte aligned) of device memory once
+ * and writes nothing (sink: a scratch buffer of at least 4 MiB that a sentinel
+ * test keeps the loads alive for).  No counterpart in the reference: a
+ * measurement aid that gives the HBM read rate reachable for that many bytes
+ * in back-to-back launches, the practical ceiling of a weight-streaming GEMM
+ * of the same size. */
+int mm_stream_read(const void* p, size_t bytes, uint32_t* sink, size_t sink_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -517,8 +517,11 @@ k_splitk_reduce(const float* __restrict__ part, int ks, int M, int N, f16* __res
 // ===========================================================================
 // Host-side planning
 // ===========================================================================
-#ifndef MM_SK_NW
-#define MM_SK_NW 8          // waves per skinny block (power of two)
+#ifndef MM_SK_NW1
+#define MM_SK_NW1 8         // waves per skinny block, M <= 16 (power of two)
+#endif
+#ifndef MM_SK_NW2
+#define MM_SK_NW2 8         // waves per skinny block, 16 < M <= 32
 #endif
 #ifndef MM_SK_SPW1
 #define MM_SK_SPW1 8        // 32-k steps per wave per round, M <= 16
@@ -532,10 +535,13 @@ k_splitk_reduce(const float* __restrict__ part, int ks, int M, int N, f16* __res
 #ifndef MM_SK_NOSPLIT_TILES
 #define MM_SK_NOSPLIT_TILES 200   // column tiles from which the K range is not split
 #endif
+#ifndef MM_SK_NOSPLIT_TILES1
+#define MM_SK_NOSPLIT_TILES1 96   // the same for M <= 16
+#endif
 #ifndef MM_SK_MAXBLOCKS
 #define MM_SK_MAXBLOCKS 2048
 #endif
-constexpr int SK_NW = MM_SK_NW;
+template <int MT> constexpr int sk_nw() { return MT == 1 ? MM_SK_NW1 : MM_SK_NW2; }
 template <int MT> constexpr int sk_spw() { return MT == 1 ? MM_SK_SPW1 : MM_SK_SPW2; }
 // One 64-column virtual-tile quad per block: more column tiles means fewer
 // K splits (less partial-sum traffic) for the same parallelism.
@@ -552,7 +558,7 @@ SkinnyPlan plan_skinny(int M, int N, int K) {
   const int nt = 1;
   const int spw = M <= 16 ? sk_spw<1>() : sk_spw<2>();
   const int nsteps = (K / 8 + 3) / 4;                  // 32-k steps
-  const int slab = SK_NW * spw;                        // steps per block round
+  const int slab = (M <= 16 ? sk_nw<1>() : sk_nw<2>()) * spw;   // steps per block round
   const int blocks_k = mm_cdiv(nsteps, slab);          // block-rounds along K
   p.ntiles = mm_cdiv(N, nt * SK_COLS);
   // One round per block (every load of a wave in flight at once) unless that
@@ -563,8 +569,10 @@ SkinnyPlan plan_skinny(int M, int N, int K) {
   // With this many column tiles the grid already spreads over the CUs: a K
   // split would only add the hand-off and a second round of blocks (two
   // 8-wave blocks are resident per CU).  Measured on MI355X at M=1:
-  // 4096x28672 16.8 -> 13.3 us, 4096x14336 10.0 -> 8.3 us.
-  if (p.ntiles >= MM_SK_NOSPLIT_TILES) ks = 1;
+  // 4096x28672 16.8 -> 13.3 us, 4096x14336 10.0 -> 8.3 us; for M <= 16
+  // from 96 tiles: 4096x6144 6.6 -> 5.6 us (two rounds per wave cost less
+  // than the split-K hand-off).
+  if (p.ntiles >= (M <= 16 ? MM_SK_NOSPLIT_TILES1 : MM_SK_NOSPLIT_TILES)) ks = 1;
   if (M > 16 && ks > MM_SK_KS2) ks = MM_SK_KS2;
   if (ks < 1) ks = 1;
   p.nrounds = mm_cdiv(blocks_k, ks);
@@ -611,7 +619,7 @@ int launch_skinny(const f16* A, int lda, const uint32_t* B, const f16* S, const 
   constexpr int SPW = sk_spw<MT>();
   const int fl = flush_steps(g, SPW);
 #define MM_LAUNCH_SK(FLV)                                                                   \
-  hipLaunchKernelGGL((k_skinny<INT4, MT, NT, SPW, SK_NW, FLV, ACT>), grid, dim3(SK_NW * 64), 0, \
+  hipLaunchKernelGGL((k_skinny<INT4, MT, NT, SPW, sk_nw<MT>(), FLV, ACT>), grid, dim3(sk_nw<MT>() * 64), 0, \
                      st, A, lda, B, S, Z, B2, S2, Z2, C, ldc, M, N, K, g, p.nrounds, part,       \
                      counters, mp ? *mp : none)
   switch (fl) {

@@ -41,6 +41,7 @@ SIGNATURES: dict[str, tuple] = {
     "mm_moe_grouped_gemm": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _vp, _c_int,
                                      _c_int, _c_int, _c_int, _c_int, _vp, _vp]),
     "mm_moe_combine": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _vp]),
+    "mm_stream_read": (_c_int, [_vp, _c_size, _vp, _c_size, _vp]),
 }
 
 _lib = None

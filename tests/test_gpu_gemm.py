@@ -191,3 +191,16 @@ def test_split_k_large_and_nonfinite_partials(M, K):
     fin = torch.isfinite(ref)
     err = (out[fin] - ref[fin]).abs().max().item()
     assert err <= TOL * ref[fin].abs().max().item()
+
+
+def test_stream_read_measurement_aid():
+    """mm_stream_read reads and writes nothing; misaligned sizes are refused."""
+    from mmfp4 import _lib
+    buf = torch.arange(1 << 18, dtype=torch.int32, device="cuda")
+    sink = torch.zeros(8192 * 512, dtype=torch.int32, device="cuda")
+    st = torch.cuda.current_stream().cuda_stream
+    _lib.call("mm_stream_read", buf.data_ptr(), buf.numel() * 4, sink.data_ptr(), sink.numel() * 4, st)
+    torch.cuda.synchronize()
+    assert int(sink.abs().sum()) == 0
+    with pytest.raises(ValueError):
+        _lib.call("mm_stream_read", buf.data_ptr(), 1000, sink.data_ptr(), sink.numel() * 4, st)
