@@ -122,17 +122,23 @@ int mm_moe_sort(const int32_t* expert_ids, int T, int k, int E, int32_t* offsets
 int mm_moe_sort_i64(const int64_t* expert_ids, int T, int k, int E, int32_t* offsets,
                     int32_t* sorted_idx, int32_t* inverse, void* stream);
 
+/* Bytes of workspace mm_moe_router needs for T tokens (zeroed once before
+ * first use; the kernel leaves its arrival counters at zero).  It may be the
+ * same buffer as the GEMMs' workspace on the same stream. */
+size_t mm_moe_router_workspace_bytes(int T, int H, int E);
+
 /* Router: logits = X[T, H] . W[E, H]^T (+ bias[E] fp32, may be NULL), fp32
  * accumulate, rounded to fp16 (the gate nn.Linear's output dtype); fp32
  * softmax over the E experts; top-k descending (lower expert id first on
  * ties); renorm != 0 divides the k probabilities by their sum.  ids int64
- * [T, k], probs fp32 [T, k].  One launch.  Requires H % 32 == 0, E <= 4096,
+ * [T, k], probs fp32 [T, k].  One launch.  Requires H % 32 == 0, E <= 1024,
  * 1 <= k <= min(E, 64); X, W 16-byte aligned.  Replaces
  * metal_marlin/moe_dispatch.py:178-219 (_fused_router_topk) and :328-449
  * (_fused_router_topk_metal, kernel moe_fused_router_sorted), and
  * metal_marlin/kernels/moe.py:729-740 (moe_router_topk). */
 int mm_moe_router(const uint16_t* X, const uint16_t* W, const float* bias, int T, int H, int E,
-                  int k, int renorm, int64_t* ids, float* probs, void* stream);
+                  int k, int renorm, int64_t* ids, float* probs, void* ws, size_t ws_bytes,
+                  void* stream);
 
 /* Softmax + top-k of given logits [T, E] (fp16, or fp32 when logits_f32),
  * same selection and outputs as mm_moe_router.  Replaces

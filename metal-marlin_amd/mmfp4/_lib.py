@@ -35,8 +35,9 @@ SIGNATURES: dict[str, tuple] = {
                                    _c_size, _vp]),
     "mm_moe_sort": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp]),
     "mm_moe_sort_i64": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp]),
+    "mm_moe_router_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int]),
     "mm_moe_router": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _vp, _vp,
-                               _vp]),
+                               _vp, _c_size, _vp]),
     "mm_softmax_topk": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp]),
     "mm_moe_grouped_gemm": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _vp, _c_int,
                                      _c_int, _c_int, _c_int, _c_int, _vp, _vp]),

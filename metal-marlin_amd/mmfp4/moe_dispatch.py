@@ -123,8 +123,10 @@ def _router(hidden: torch.Tensor, weight_eh: torch.Tensor, bias: torch.Tensor | 
     b = None if bias is None else bias.to(torch.float32).contiguous()
     ids = torch.empty((T, top_k), dtype=torch.int64, device=dev)
     probs = torch.empty((T, top_k), dtype=torch.float32, device=dev)
+    ws = _lib.workspace(dev, int(_lib.load().mm_moe_router_workspace_bytes(T, H, E)))
     _lib.call("mm_moe_router", _lib.ptr(x), _lib.ptr(w), _lib.ptr(b), T, H, E, top_k,
-              int(renormalize), _lib.ptr(ids), _lib.ptr(probs), _lib.stream_of(x))
+              int(renormalize), _lib.ptr(ids), _lib.ptr(probs), _lib.ptr(ws), ws.numel(),
+              _lib.stream_of(x))
     return probs, ids
 
 

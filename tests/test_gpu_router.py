@@ -47,7 +47,7 @@ def _ref_probs(logits16):
 
 @pytest.mark.parametrize("T,H,E,k", [(1, 2048, 128, 8), (15, 2048, 128, 8), (17, 2048, 128, 8),
                                      (1024, 2048, 128, 8), (33, 4096, 8, 2), (40, 512, 60, 4),
-                                     (9, 256, 1000, 8)])
+                                     (9, 256, 1000, 8), (300, 7168, 256, 8), (5, 96, 16, 1)])
 def test_fused_router_vs_oracle(rng, T, H, E, k):
     import mmfp4
     x = rng.normal(0, 1, (T, H)).astype(np.float16)
