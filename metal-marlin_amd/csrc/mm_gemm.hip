@@ -111,7 +111,7 @@ k_skinny(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
                 : (t == 0 ? SkTile{B, S, Z, n0} : SkTile{B2, S2, Z2, n0});
   skinny_wave<INT4, MT, NT, SPW, FL>(A, lda, nullptr, 1, M, tl, N, K, g, blk_st0 + wave * SPW,
                                      nrounds, NW * SPW, acc);
-  skinny_block_reduce<MT, NT, NW>(red, acc);
+  skinny_block_reduce<MT, NT, NW>(red, acc, M);
 
   // Lane (c, q) of wave 0 holds rows 16*mt + 4*q + rr, columns 4*c + j of
   // each tile.
@@ -240,7 +240,7 @@ k_strip(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
   for (int t = 0; t < NS; ++t) acc[t] = f32x4{0, 0, 0, 0};
   strip_wave<INT4, NS, SPW, FL>(A, lda, nullptr, 1, M, B, S, Z, N, K, g, n0, wave * SPW,
                                 nrounds, NW * SPW, acc);
-  strip_block_reduce<NS, NW>(red, acc);
+  strip_block_reduce<NS, NW>(red, acc, M);
   if (wave != 0) return;
   const int m = lane & 15, kb = lane >> 4;
   if (m >= M) return;

@@ -205,7 +205,7 @@ k_moe_grouped(const f16* __restrict__ X, const int32_t* __restrict__ sorted_idx,
     skinny_wave<false, MT, NT, MOE_SPW, FL>(A, K, gather ? sorted_idx + mb : nullptr, topk, mrows,
                                             tl, N, K, g, wave * MOE_SPW, nrounds,
                                             MOE_NW * MOE_SPW, acc);
-    skinny_block_reduce<MT, NT, MOE_NW>(red, acc);
+    skinny_block_reduce<MT, NT, MOE_NW>(red, acc, mrows);
     if (wave == 0) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)

@@ -236,33 +236,40 @@ MM_DEV void skinny_wave(const f16* __restrict__ A, int lda, const int* __restric
 // Every wave but wave 0 parks its accumulators in LDS ((NW-1) tiles), one
 // barrier, then wave 0 adds them in wave order (deterministic).  On return
 // wave 0 holds the block sum; the other waves' values are unspecified.
+// Only the lanes that hold rows < mrows move data (lane (c, q) holds rows
+// 16*mt + 4*q .. + 3): at M = 1 that is a quarter of the LDS traffic.
 template <int MT, int NT, int NW>
-MM_DEV void skinny_block_reduce(float* red, f32x4 (&acc)[MT][NT][4]) {
+MM_DEV void skinny_block_reduce(float* red, f32x4 (&acc)[MT][NT][4], int mrows) {
   constexpr int TILE = MT * NT * 16 * 64;   // floats per wave: 16 per lane per (mt, t)
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int q = lane >> 4;
   if (wave > 0) {
     float* dst = red + (size_t)(wave - 1) * TILE;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int t = 0; t < NT; ++t)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          *(f32x4*)(dst + (((mt * NT + t) * 4 + j) * 64 + lane) * 4) = acc[mt][t][j];
-  }
-  __syncthreads();
-  if (wave == 0) {
-#pragma unroll
-    for (int w = 0; w < NW - 1; ++w) {
-      const float* src = red + (size_t)w * TILE;
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
+      if (mt * 16 + 4 * q < mrows) {
 #pragma unroll
         for (int t = 0; t < NT; ++t)
 #pragma unroll
           for (int j = 0; j < 4; ++j)
-            acc[mt][t][j] += *(const f32x4*)(src + (((mt * NT + t) * 4 + j) * 64 + lane) * 4);
-    }
+            *(f32x4*)(dst + (((mt * NT + t) * 4 + j) * 64 + lane) * 4) = acc[mt][t][j];
+      }
+  }
+  __syncthreads();
+  if (wave == 0) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+      if (mt * 16 + 4 * q < mrows) {
+#pragma unroll
+        for (int w = 0; w < NW - 1; ++w) {
+          const float* src = red + (size_t)w * TILE;
+#pragma unroll
+          for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              acc[mt][t][j] += *(const f32x4*)(src + (((mt * NT + t) * 4 + j) * 64 + lane) * 4);
+        }
+      }
   }
 }
 
@@ -381,17 +388,19 @@ MM_DEV void strip_wave(const f16* __restrict__ A, int lda, const int* __restrict
 }
 
 // Every wave but wave 0 parks its accumulators in LDS, one barrier, then
-// wave 0 adds them in wave order (deterministic).
+// wave 0 adds them in wave order (deterministic).  Only lanes of rows < M
+// (row = lane & 15) move data.
 template <int NS, int NW>
-MM_DEV void strip_block_reduce(float* red, f32x4 (&acc)[NS]) {
+MM_DEV void strip_block_reduce(float* red, f32x4 (&acc)[NS], int M) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  if (wave > 0) {
+  const bool live = (lane & 15) < M;
+  if (wave > 0 && live) {
 #pragma unroll
     for (int t = 0; t < NS; ++t)
       *(f32x4*)(red + (((size_t)(wave - 1) * NS + t) * 64 + lane) * 4) = acc[t];
   }
   __syncthreads();
-  if (wave == 0) {
+  if (wave == 0 && live) {
 #pragma unroll
     for (int w = 0; w < NW - 1; ++w)
 #pragma unroll
