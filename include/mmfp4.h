@@ -167,6 +167,21 @@ int mm_moe_grouped_gemm(const uint16_t* X, const int32_t* sorted_idx, const int3
 int mm_moe_combine(const uint16_t* Y, const float* probs, const int32_t* inverse, int T, int k,
                    int H, uint16_t* out, void* stream);
 
+/* Routed-expert SwiGLU MLP over all experts in one call:
+ *   h = X[t] . W_gu[e] ([E, H/8, 2I] packed, scales [E, H/g, 2I]);
+ *   a = silu(h[:I]) * h[I:];  y = a . W_dn[e] ([E, I/8, H], scales [E, I/g, H]);
+ *   out[t] = sum_j probs[t, j] * y(t, j)   (fp32, slot order; fp16 [T, H]).
+ * expert_ids [T, k] int32 (ids_i64 = 0) or int64 (ids_i64 = 1); probs fp32
+ * [T, k].  Scratch the caller provides: act_buf fp16 [T*k, I], y_buf fp16
+ * [T*k, H], sort_buf int32 [E + 1 + 2*T*k].  Four launches (sort, gate_up,
+ * down, combine), the same as mm_moe_sort + 2 x mm_moe_grouped_gemm +
+ * mm_moe_combine.  Replaces metal_marlin/moe_dispatch.py:1241-1431
+ * (_fused_expert_mlp) with the combine of :812-925. */
+int mm_moe_mlp_fp4(const uint16_t* X, const void* expert_ids, int ids_i64, const float* probs,
+                   int T, int k, int E, int H, int I, const uint32_t* Bgu, const uint16_t* Sgu,
+                   const uint32_t* Bdn, const uint16_t* Sdn, int group_size, uint16_t* act_buf,
+                   uint16_t* y_buf, int32_t* sort_buf, uint16_t* out, void* stream);
+
 /* ------------------------------------------------------------ measurement */
 
 /* Reads `bytes` (a multiple of 16, 16-byte aligned) of device memory once

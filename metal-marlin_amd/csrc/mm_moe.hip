@@ -514,3 +514,45 @@ extern "C" int mm_moe_combine(const uint16_t* Y, const float* probs, const int32
   MM_CHECK_LAUNCH("mm_moe_combine");
   return 0;
 }
+
+// Routed-expert SwiGLU MLP in one call: stable sort -> gate_up (token gather
+// + SwiGLU epilogue) -> down -> probability-weighted combine, four launches
+// on one stream with no host synchronisation.  (Deriving each expert's rows
+// from the ids inside the GEMM blocks instead of sorting was measured and
+// rejected: no faster at T=32 and 20% slower at T=128, since every block
+// then scans all T*k ids before its first load.)
+template <typename IdT>
+int moe_mlp(const uint16_t* X, const IdT* ids, const float* probs, int T, int k, int E, int H,
+            int I, const uint32_t* Bgu, const uint16_t* Sgu, const uint32_t* Bdn,
+            const uint16_t* Sdn, int g, uint16_t* act_buf, uint16_t* y_buf, int32_t* sort_buf,
+            uint16_t* out, void* stream) {
+  MM_CHECK_ARG(T >= 0 && k > 0 && E > 0 && H > 0 && I > 0, "mm_moe_mlp_fp4: bad shape");
+  if (T == 0) return 0;
+  MM_CHECK_ARG(act_buf != nullptr && y_buf != nullptr && sort_buf != nullptr && out != nullptr,
+               "mm_moe_mlp_fp4: scratch and output buffers are required");
+  const long tk = (long)T * k;
+  int32_t* offsets = sort_buf;
+  int32_t* sorted_idx = sort_buf + E + 1;
+  int32_t* inverse = sorted_idx + tk;
+  int rc = moe_sort("mm_moe_mlp_fp4", ids, T, k, E, offsets, sorted_idx, inverse, stream);
+  if (rc) return rc;
+  rc = mm_moe_grouped_gemm(X, sorted_idx, offsets, 1, k, T, Bgu, Sgu, E, H, 2 * I, g, 1, act_buf,
+                           stream);
+  if (rc) return rc;
+  rc = mm_moe_grouped_gemm(act_buf, sorted_idx, offsets, 0, k, T, Bdn, Sdn, E, I, H, g, 0, y_buf,
+                           stream);
+  if (rc) return rc;
+  return mm_moe_combine(y_buf, probs, inverse, T, k, H, out, stream);
+}
+
+extern "C" int mm_moe_mlp_fp4(const uint16_t* X, const void* expert_ids, int ids_i64,
+                              const float* probs, int T, int k, int E, int H, int I,
+                              const uint32_t* Bgu, const uint16_t* Sgu, const uint32_t* Bdn,
+                              const uint16_t* Sdn, int g, uint16_t* act_buf, uint16_t* y_buf,
+                              int32_t* sort_buf, uint16_t* out, void* stream) {
+  if (ids_i64)
+    return moe_mlp<int64_t>(X, (const int64_t*)expert_ids, probs, T, k, E, H, I, Bgu, Sgu, Bdn, Sdn,
+                            g, act_buf, y_buf, sort_buf, out, stream);
+  return moe_mlp<int32_t>(X, (const int32_t*)expert_ids, probs, T, k, E, H, I, Bgu, Sgu, Bdn, Sdn,
+                          g, act_buf, y_buf, sort_buf, out, stream);
+}

@@ -42,6 +42,8 @@ SIGNATURES: dict[str, tuple] = {
     "mm_moe_grouped_gemm": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _vp, _c_int,
                                      _c_int, _c_int, _c_int, _c_int, _vp, _vp]),
     "mm_moe_combine": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _vp]),
+    "mm_moe_mlp_fp4": (_c_int, [_vp, _vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_int, _c_int,
+                                _vp, _vp, _vp, _vp, _c_int, _vp, _vp, _vp, _vp, _vp]),
     "mm_stream_read": (_c_int, [_vp, _c_size, _vp, _c_size, _vp]),
 }
 

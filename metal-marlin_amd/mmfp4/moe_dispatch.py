@@ -228,21 +228,39 @@ def moe_expert_gemm_fp4(activations: torch.Tensor, expert_weights: torch.Tensor,
 def moe_mlp_fp4(hidden: torch.Tensor, gate_up_packed: torch.Tensor, gate_up_scales: torch.Tensor,
                 down_packed: torch.Tensor, down_scales: torch.Tensor, expert_ids: torch.Tensor,
                 expert_probs: torch.Tensor, group_size: int = 128) -> torch.Tensor:
-    """Routed-expert SwiGLU MLP over all experts in four launches:
+    """Routed-expert SwiGLU MLP over all experts, one library call
+    (`mm_moe_mlp_fp4`):
         h = x @ W_gu[e];  a = silu(h[:, :I]) * h[:, I:];  y = a @ W_dn[e];
         out[t] = sum_j p[t, j] * y[(t, j)]
     (moe_dispatch.py:1241-1431 per expert, combined as :812-925).
-    gate_up_packed [E, H/8, 2I], down_packed [E, I/8, H]; scales alike."""
-    _lib.require_device(hidden, gate_up_packed, gate_up_scales, down_packed, down_scales,
-                        expert_ids, expert_probs)
+    gate_up_packed [E, H/8, 2I], down_packed [E, I/8, H]; scales alike.
+    Four launches on the caller's stream (sort, gate_up, down, combine)."""
+    dev = _lib.require_device(hidden, gate_up_packed, gate_up_scales, down_packed, down_scales,
+                              expert_ids, expert_probs)
     T, k = expert_ids.shape
-    E = gate_up_packed.shape[0]
+    E, HP, N2 = gate_up_packed.shape
+    H, I = HP * 8, N2 // 2
+    if tuple(down_packed.shape) != (E, I // 8, H):
+        raise ValueError(f"down_packed shape {tuple(down_packed.shape)} != ({E}, {I // 8}, {H})")
+    for name, sc, kk, nn in (("gate_up_scales", gate_up_scales, H, N2),
+                             ("down_scales", down_scales, I, H)):
+        if tuple(sc.shape) != (E, kk // group_size, nn):
+            raise ValueError(f"{name} shape {tuple(sc.shape)} != ({E}, {kk // group_size}, {nn})")
     x = _half(hidden.reshape(T, -1))
-    s_idx, offs, inv = _sort(expert_ids, E)
-    a = _grouped(x, s_idx, offs, True, k, T, gate_up_packed, _half(gate_up_scales), group_size, 1)
-    y = _grouped(a, s_idx, offs, False, k, T, down_packed, _half(down_scales), group_size, 0)
-    info = MoEDispatchInfo(s_idx, s_idx, offs, inv, T, k, E, s_idx)
-    return scatter_expert_outputs(y, expert_probs, info).to(hidden.dtype)
+    if x.shape[-1] != H:
+        raise ValueError(f"hidden size {x.shape[-1]} != packed K={H}")
+    i64 = expert_ids.dtype == torch.int64
+    ids = expert_ids.contiguous() if i64 else expert_ids.to(torch.int32).contiguous()
+    p = expert_probs.to(torch.float32).contiguous()
+    act = torch.empty((T * k, I), dtype=torch.float16, device=dev)
+    y = torch.empty((T * k, H), dtype=torch.float16, device=dev)
+    sort_buf = torch.empty(E + 1 + 2 * T * k, dtype=torch.int32, device=dev)
+    out = torch.empty((T, H), dtype=torch.float16, device=dev)
+    _lib.call("mm_moe_mlp_fp4", _lib.ptr(x), _lib.ptr(ids), int(i64), _lib.ptr(p), T, k, E, H, I,
+              _lib.ptr(gate_up_packed.contiguous()), _lib.ptr(_half(gate_up_scales)),
+              _lib.ptr(down_packed.contiguous()), _lib.ptr(_half(down_scales)), group_size,
+              _lib.ptr(act), _lib.ptr(y), _lib.ptr(sort_buf), _lib.ptr(out), _lib.stream_of(x))
+    return out if hidden.dtype == torch.float16 else out.to(hidden.dtype)
 
 
 class MoEDispatcher(nn.Module):

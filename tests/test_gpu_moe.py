@@ -183,3 +183,27 @@ def test_gpu_grouping_api(rng, T, k, E):
     assert max_abs_rel(out, ref) <= TOL
     with pytest.raises(ValueError):
         mmfp4.GPUExpertGrouping(E, device="cpu")
+
+
+
+@pytest.mark.parametrize("E,T,k,H,I,i64", [(128, 32, 8, 2048, 768, True), (16, 1, 4, 256, 128, False),
+                                          (64, 256, 8, 512, 256, True), (8, 3, 8, 256, 128, False)])
+def test_moe_mlp_one_call_matches_steps(rng, E, T, k, H, I, i64):
+    """mm_moe_mlp_fp4 (one library call) is bit-identical to the sort ->
+    grouped GEMM -> grouped GEMM -> combine steps on the same inputs."""
+    import mmfp4
+    from mmfp4 import moe_dispatch as md
+    g = 128
+    GU, GS = _experts(rng, E, H, 2 * I, g)
+    DP, DS = _experts(rng, E, I, H, g)
+    x = to_dev(rng.normal(0, 1, (T, H)).astype(np.float16))
+    ids, probs = omoe.router_topk(rng.normal(0, 1, (T, E)).astype(np.float32), k)
+    dids = to_dev(ids.astype(np.int64 if i64 else np.int32))
+    dp = to_dev(probs)
+    announce(f"moe mlp one call vs steps E={E} T={T} k={k} i64={i64}")
+    fused = mmfp4.moe_mlp_fp4(x, to_dev(GU), to_dev(GS), to_dev(DP), to_dev(DS), dids, dp, g)
+    s_idx, offs, inv = md._sort(dids, E)
+    a = md._grouped(x, s_idx, offs, True, k, T, to_dev(GU), to_dev(GS), g, 1)
+    y = md._grouped(a, s_idx, offs, False, k, T, to_dev(DP), to_dev(DS), g, 0)
+    ref = md.scatter_expert_outputs(y, dp, md.MoEDispatchInfo(s_idx, s_idx, offs, inv, T, k, E, s_idx))
+    assert torch.equal(fused, ref)
