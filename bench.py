@@ -417,6 +417,9 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--all", action="store_true", help="accepted for compatibility; every "
                     "BASELINE config is reported by default")
+    ap.add_argument("--section", choices=("all", "layer", "prefill", "moe"), default="all",
+                    help="run one workload alone (for profiling); the default runs all and "
+                         "prints the contract line")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="no timing: run a 512 MiB copy (counter calibration) then the M=1 layer "
                          "GEMMs and the M=2048 prefill GEMMs, for rocprofv3 --pmc runs")
@@ -436,6 +439,21 @@ def main() -> int:
     if args.pmc_probe:
         return pmc_probe(torch, mmfp4)
     torch.cuda.synchronize()
+    if args.section != "all":
+        # One workload alone, for a clean rocprofv3 kernel trace of it.
+        if args.section == "layer":
+            r = run_layer_bench(torch, mmfp4, 1, args.steps, args.warmup)
+            res = {"us_per_step": round(1e3 * r["ms_per_step"], 3), "per_shape": r["per_shape"],
+                   "TBps": round(r["step_bytes"] / (r["ms_per_step"] * 1e-3) / 1e12, 4)}
+        elif args.section == "prefill":
+            r = run_prefill_bench(torch, mmfp4, 2048, max(5, args.steps // 20),
+                                  max(2, args.warmup // 10))
+            res = {"ms_per_step": round(r["ms_per_step"], 4), "per_shape": r["per_shape"],
+                   "TFLOPs": round(r["flops"] / (r["ms_per_step"] * 1e-3) / 1e12, 1)}
+        else:
+            res = [run_moe_bench(torch, mmfp4, T, 20) for T in (32, 1024)]
+        print(json.dumps({"section": args.section, "result": res}))
+        return 0
     layer = run_layer_bench(torch, mmfp4, 1, args.steps, args.warmup)
     pre = run_prefill_bench(torch, mmfp4, 2048, max(5, args.steps // 20), max(2, args.warmup // 10))
     value_tbs = layer["step_bytes"] / (layer["ms_per_step"] * 1e-3) / 1e12
