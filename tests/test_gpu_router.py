@@ -120,3 +120,41 @@ def test_moe_dispatcher_forward_matches_torch():
             for j in range(k):
                 ref[t] += w[t, j].float() * experts[int(i[t, j])](x[t:t + 1]).float()[0]
     assert (out - ref).abs().max().item() <= 1e-2 * ref.abs().max().item()
+
+
+@pytest.mark.parametrize("E,k,dtype", [(16, 1, np.float32), (16, 16, np.float16), (128, 64, np.float32),
+                                       (200, 8, np.float16), (300, 16, np.float32),
+                                       (1000, 8, np.float16), (2000, 32, np.float32)])
+def test_softmax_topk_layouts(rng, E, k, dtype):
+    """Every selection layout of the softmax/top-k kernel: 16 lanes per token
+    (E <= 256, up to 16 slots per lane, k up to 64), 64 lanes per token with
+    registers (E <= 1024) and the per-round path (E > 1024); odd token counts
+    so the last wave holds fewer than four tokens."""
+    import mmfp4
+    T = 37
+    logits = rng.normal(0, 2, (T, E)).astype(dtype)
+    logits[3, :] = 0.5                          # all equal: the lowest ids win
+    announce(f"softmax_topk layouts E={E} k={k} {np.dtype(dtype).name}")
+    p, ids = mmfp4.router_softmax_topk(to_dev(logits), k, renormalize=True)
+    ref = _ref_probs(logits)
+    _check_topk(ids, p.float(), ref, k, True)
+    assert to_np(ids)[3].tolist() == list(range(k))
+
+
+@pytest.mark.parametrize("T,H,E,k", [(40, 256, 300, 8), (19, 512, 64, 64), (33, 128, 16, 3)])
+def test_fused_router_bias_and_layouts(rng, T, H, E, k):
+    """Router with a gate bias (added to the fp32 logits before the fp16
+    rounding, as nn.Linear does) over the 16-lane and 64-lane top-k layouts."""
+    import mmfp4
+    x = rng.normal(0, 1, (T, H)).astype(np.float16)
+    w = (rng.normal(0, 1, (E, H)) / np.sqrt(H)).astype(np.float16)
+    b = rng.normal(0, 0.5, E).astype(np.float16)
+    logits16 = (x.astype(np.float32) @ w.astype(np.float32).T + b.astype(np.float32)).astype(np.float16)
+    ref = _ref_probs(logits16)
+    gate = torch.nn.Linear(H, E, bias=True).to("cuda").half()
+    with torch.no_grad():
+        gate.weight.copy_(to_dev(w))
+        gate.bias.copy_(to_dev(b))
+    announce(f"fused router bias T={T} H={H} E={E} k={k}")
+    wts, ids = mmfp4.fused_router_topk(to_dev(x), gate, k)
+    _check_topk(ids, wts.float(), ref, k, True)
