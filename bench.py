@@ -480,7 +480,7 @@ def main() -> int:
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic("k_skinny_llama3_layer_m1.md"),
                      "traffic_source": "profiles/k_skinny_llama3_layer_m1.md",
-                     "kernel": "k_skinny + k_strip (M<=16 decode path, 4 launches per layer)",
+                     "kernel": "k_skinny + k_skinny_dual (M<=16 decode path, 4 launches per layer)",
                      "launch_us_avg": round(layer["launch_us_avg"], 3)},
         "per_shape_m1": layer["per_shape"],
         "prefill_m2048": {"tflops": round(tflops, 1), "frac_fp16_peak": round(tflops /

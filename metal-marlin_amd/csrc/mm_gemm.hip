@@ -225,6 +225,49 @@ k_skinny(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
     __hip_atomic_store(&counters[blockIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Two-slab skinny kernel (M <= 8, K % 64 == 0, group size % 64 == 0): one
+// block per 32 columns over the whole K, no split-K hand-off.  Each MFMA
+// 16x16x32 step covers 64 k: rows 0..7 of the operand carry the activations
+// of the first 32-k slab against columns 0..7 (weights of that slab), rows
+// 8..15 the second slab against columns 8..15, so D[m][c] + D[8+m][8+c] is
+// row m of the product for column group c.  Half-width tiles double the
+// grid of narrow layers without a K split.
+template <bool INT4, int SPW, int NW, int FL>
+__global__ void __launch_bounds__(NW * 64)
+k_skinny_dual(const f16* __restrict__ A, const uint32_t* __restrict__ B,
+              const f16* __restrict__ S, const f16* __restrict__ Z, f16* __restrict__ C, int M,
+              int N, int K, int g, int nrounds) {
+  __shared__ float red[(NW - 1) * 16 * 64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c = lane & 15, q = lane >> 4;
+  const int n0 = blockIdx.x * 32;
+  f32x4 acc[1][1][4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) acc[0][0][j] = f32x4{0, 0, 0, 0};
+  const SkTile tl[1] = {SkTile{B, S, Z, n0}};
+  skinny_wave<INT4, 1, 1, SPW, FL, true>(A, K, nullptr, 1, M, tl, N, K, g, wave * SPW, nrounds,
+                                         NW * SPW, acc);
+  // Rows 8..15 (lanes q >= 2) hold the second slab's sums: reduce all 16.
+  skinny_block_reduce<1, 1, NW>(red, acc, 16);
+  if (wave != 0) return;
+  // Lane (q, c) with q < 2, c < 8 adds lane (q + 2, c + 8) = lane + 40.
+  f32x4 v[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) v[j][r] = acc[0][0][j][r] + __shfl_down(acc[0][0][j][r], 40);
+  if (q >= 2 || c >= 8) return;
+  const int col = n0 + 4 * c;
+  if (col >= N) return;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int row = 4 * q + r;
+    if (row < M)
+      *(f16x4*)(C + (size_t)row * N + col) =
+          f16x4{(f16)v[0][r], (f16)v[1][r], (f16)v[2][r], (f16)v[3][r]};
+  }
+}
+
 // Column-strip kernel (M <= 16, group size a multiple of 32): one block per
 // NS*16 columns over the whole K; no split-K and no workspace.
 template <bool INT4, int NS, int SPW, int NW, int FL>
@@ -634,6 +677,58 @@ int launch_skinny(const f16* A, int lda, const uint32_t* B, const f16* S, const 
   return 0;
 }
 
+#ifndef MM_SK_DUAL
+#define MM_SK_DUAL 1
+#endif
+#ifndef MM_SK_DUAL_SMALL
+#define MM_SK_DUAL_SMALL 1   // also small layers (K*N <= 4096^2) the 64-column plan would split
+#endif
+#ifndef MM_SK_DUAL_NW
+#define MM_SK_DUAL_NW 8
+#endif
+// The two-slab kernel serves M <= 8 layers whose 64-column plan runs unsplit
+// on fewer than MM_SK_DUAL_BELOW blocks, when 32-column tiles give at least
+// MM_SK_DUAL_MIN_TILES blocks (measured on MI355X at M=1: 4096 -> 6144
+// 6.6 -> 5.3 us; 14336 -> 4096, which the 64-column plan splits 7 ways, is
+// slower as 128 unsplit blocks, 9.3 -> 11.1 us, and keeps the split).  Small
+// layers (K*N <= 4096^2) take it even where the 64-column plan would split:
+// 4096 -> 4096 4.9 us against 5.2-5.3 us for the column-strip kernel.
+#ifndef MM_SK_DUAL_BELOW
+#define MM_SK_DUAL_BELOW 128
+#endif
+#ifndef MM_SK_DUAL_MIN_TILES
+#define MM_SK_DUAL_MIN_TILES 96
+#endif
+
+bool use_dual(int M, int N, int K, int g) {
+  if (!MM_SK_DUAL || M > 8 || K % 64 != 0 || g % 64 != 0 || N % 4 != 0) return false;
+  if (flush_steps(g / 2, sk_spw<1>()) == 0) return false;
+  return (plan_skinny(M, N, K).ksplit == 1 || (MM_SK_DUAL_SMALL && (long)K * N <= 4096L * 4096)) &&
+         mm_cdiv(N, SK_COLS) < MM_SK_DUAL_BELOW && mm_cdiv(N, 32) >= MM_SK_DUAL_MIN_TILES;
+}
+
+template <bool INT4>
+int launch_dual(const f16* A, const uint32_t* B, const f16* S, const f16* Z, f16* C, int M, int N,
+                int K, int g, hipStream_t st) {
+  constexpr int SPW = sk_spw<1>(), NW = MM_SK_DUAL_NW;
+  const int nsteps = K / 64;                           // 64-k steps
+  const int nrounds = mm_cdiv(nsteps, NW * SPW);
+  const int fl = flush_steps(g / 2, SPW);              // 64-k steps per scale group
+#define MM_LAUNCH_DU(FLV)                                                                      \
+  hipLaunchKernelGGL((k_skinny_dual<INT4, SPW, NW, FLV>), dim3(mm_cdiv(N, 32)), dim3(NW * 64), 0, \
+                     st, A, B, S, Z, C, M, N, K, g, nrounds)
+  switch (fl) {
+    case 1: MM_LAUNCH_DU(1); break;
+    case 2: MM_LAUNCH_DU(2); break;
+    case 4: MM_LAUNCH_DU(4); break;
+    case 8: MM_LAUNCH_DU(8 <= SPW ? 8 : 4); break;
+    default: MM_CHECK_ARG(false, "gemm(dual): unsupported group size %d", g);
+  }
+#undef MM_LAUNCH_DU
+  MM_CHECK_LAUNCH("gemm(dual)");
+  return 0;
+}
+
 #ifndef MM_ST_NW
 #define MM_ST_NW 8
 #endif
@@ -757,6 +852,7 @@ int gemm_dispatch(const char* who, const f16* A, const uint32_t* B, const f16* S
   // The decode kernels address one weight matrix with 32-bit byte offsets;
   // larger matrices take the prefill kernels (64-bit addressing) at any M.
   const bool off32 = (size_t)(K / 8) * (size_t)N * 4 < ((size_t)1 << 32);
+  if (off32 && use_dual(M, N, K, g)) return launch_dual<INT4>(A, B, S, Z, C, M, N, K, g, st);
   if (off32 && MM_ST_MODE && M <= 16 && flush_steps(g, MM_ST_SPW) > 0) {
     // Column strips (no split-K hand-off) win for small layers, where the
     // hand-off is a large share of the launch; split-K wins from ~13 MB up

@@ -100,26 +100,30 @@ struct SkTile {
 // group_size == 32*FL*k for an integer k), or 0 for pre-scale.
 // Rows >= M and columns past N compute values that are never stored: their
 // addresses are clamped into the matrix so no load is predicated.
-template <bool INT4, int MT, int NT, int SPW, int FL>
+template <bool INT4, int MT, int NT, int SPW, int FL, bool DUAL = false>
 MM_DEV void skinny_wave(const f16* __restrict__ A, int lda, const int* __restrict__ rowmap,
                         int rowdiv, int M, const SkTile (&tl)[NT], int N, int K, int g,
                         int st0, int nrounds, int ststride, f32x4 (&acc)[MT][NT][4]) {
   static_assert(FL == 0 || (SPW % FL == 0), "flush interval must divide the round");
   const int lane = threadIdx.x & 63;
   const int c = lane & 15, q = lane >> 4;
+  // DUAL: a step is 64 k; lanes c < 8 take its first 32-k slab and lanes
+  // c >= 8 the second, both for the 32 columns of lane group c & 7.
+  constexpr int SLAB = DUAL ? 2 : 1;
+  const int cl = DUAL ? (c & 7) : c, hs = DUAL ? (c >> 3) : 0;
   const int KP = K >> 3;
-  const int nsteps = (KP + 3) >> 2;
+  const int nsteps = (KP + 4 * SLAB - 1) / (4 * SLAB);
 
   uint32_t aoff[MT];                       // byte offset of A[row][0]
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
-    const int m = min(mt * 16 + c, M - 1);
+    const int m = min(mt * 16 + cl, M - 1);
     const int r = rowmap != nullptr ? rowmap[m] / rowdiv : m;
     aoff[mt] = (uint32_t)r * (uint32_t)lda * 2u;
   }
   uint32_t coff[NT];                       // column index of this lane's first column
 #pragma unroll
-  for (int t = 0; t < NT; ++t) coff[t] = (uint32_t)min(tl[t].col0 + 4 * c, N - 4);
+  for (int t = 0; t < NT; ++t) coff[t] = (uint32_t)min(tl[t].col0 + 4 * cl, N - 4);
 
   st0 = __builtin_amdgcn_readfirstlane(st0);   // wave-uniform: group indices stay scalar
   constexpr int NF = FL > 0 ? SPW / FL : 1;    // scale groups per round (post-scale)
@@ -136,7 +140,7 @@ MM_DEV void skinny_wave(const f16* __restrict__ A, int lda, const int* __restric
 #pragma unroll
       for (int f = 0; f < NF; ++f) {
         const int stg = min(stb + f * FL, nsteps - 1);
-        const uint32_t gi = (uint32_t)((stg * 32) / g);      // scalar
+        const uint32_t gi = (uint32_t)((stg * 32 * SLAB) / g);      // scalar
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
           s4[f][t] = *at_bytes<f16x4>(tl[t].S, (gi * (uint32_t)N + coff[t]) * 2u);
@@ -147,7 +151,7 @@ MM_DEV void skinny_wave(const f16* __restrict__ A, int lda, const int* __restric
     }
 #pragma unroll
     for (int i = 0; i < SPW; ++i) {
-      const int kp = min(4 * min(stb + i, nsteps - 1) + q, KP - 1);
+      const int kp = min(4 * (SLAB * min(stb + i, nsteps - 1) + hs) + q, KP - 1);
 #pragma unroll
       for (int t = 0; t < NT; ++t)
         w[i][t] = MM_SK_NT ? __builtin_nontemporal_load(at_bytes<u32x4>(tl[t].B, ((uint32_t)kp * (uint32_t)N + coff[t]) * 4u))
@@ -158,10 +162,10 @@ MM_DEV void skinny_wave(const f16* __restrict__ A, int lda, const int* __restric
     }
     // Steps past K (a partial last step, or a round overhanging the end)
     // contribute zero through a zeroed activation operand.
-    if (stb + SPW > nsteps || (K & 31) != 0) {
+    if (stb + SPW > nsteps || (K & (32 * SLAB - 1)) != 0) {
 #pragma unroll
       for (int i = 0; i < SPW; ++i) {
-        const bool valid = stb + i < nsteps && 4 * (stb + i) + q < KP;
+        const bool valid = stb + i < nsteps && 4 * (SLAB * (stb + i) + hs) + q < KP;
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
           if (!valid) a[i][mt] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
@@ -172,7 +176,7 @@ MM_DEV void skinny_wave(const f16* __restrict__ A, int lda, const int* __restric
       // Pre-scale: each lane's own group, every step.
 #pragma unroll
       for (int i = 0; i < SPW; ++i) {
-        const int kp = min(4 * min(stb + i, nsteps - 1) + q, KP - 1);
+        const int kp = min(4 * (SLAB * min(stb + i, nsteps - 1) + hs) + q, KP - 1);
         const uint32_t gi = (uint32_t)((kp * 8) / g);
 #pragma unroll
         for (int t = 0; t < NT; ++t) {

@@ -204,3 +204,27 @@ def test_stream_read_measurement_aid():
     assert int(sink.abs().sum()) == 0
     with pytest.raises(ValueError):
         _lib.call("mm_stream_read", buf.data_ptr(), 1000, sink.data_ptr(), sink.numel() * 4, st)
+
+
+@pytest.mark.parametrize("M,K,N,g,int4", [(1, 512, 3072, 128, False), (8, 4160, 3076, 64, False),
+                                          (3, 1024, 4096, 256, False), (5, 576, 6144, 64, False),
+                                          (1, 1024, 3072, 128, True), (7, 640, 4100, 64, True),
+                                          (1, 4096, 4096, 128, False), (2, 4096, 6144, 128, True)])
+def test_two_slab_decode_vs_oracle(rng, M, K, N, g, int4):
+    """The two-slab decode kernel (M <= 8, 32-column blocks, each MFMA step 64 k
+    split over operand rows 0-7 / 8-15): ragged last tile (N % 32 != 0), a
+    partial last round (K = 65 x 64), group sizes 64..256, FP4 and INT4."""
+    import mmfp4
+    w = rng.normal(0, 0.02, (N, K)).astype(np.float16)
+    a = rng.normal(0, 1, (M, K)).astype(np.float16)
+    announce(f"two-slab decode M={M} K={K} N={N} g={g} int4={int4}")
+    if int4:
+        packed, s, z = ofp4.pack_u4_weights(w, g)
+        ref = ofp4.gemm_u4_ref(a, packed, s, z, g)
+        out = to_np(mmfp4.marlin_gemm_int4(to_dev(a), to_dev(packed), to_dev(s), to_dev(z), g))
+    else:
+        packed, scales = ofp4.quantize_fp4(w, g)
+        ref = ofp4.gemm_fp4_ref(a, packed, scales, g)
+        out = to_np(mmfp4.marlin_gemm_fp4(to_dev(a), to_dev(packed), to_dev(scales), g))
+    assert out.shape == (M, N)
+    assert max_abs_rel(out, ref) <= TOL
