@@ -47,9 +47,18 @@ def _ref_probs(logits16):
 
 @pytest.mark.parametrize("T,H,E,k", [(1, 2048, 128, 8), (15, 2048, 128, 8), (17, 2048, 128, 8),
                                      (1024, 2048, 128, 8), (33, 4096, 8, 2), (40, 512, 60, 4),
-                                     (9, 256, 1000, 8), (300, 7168, 256, 8), (5, 96, 16, 1)])
-def test_fused_router_vs_oracle(rng, T, H, E, k):
+                                     (9, 256, 1000, 8), (300, 7168, 256, 8), (5, 96, 16, 1),
+                                     (4100, 2048, 128, 8)])
+@pytest.mark.parametrize("path", ["auto", "one_launch"])
+def test_fused_router_vs_oracle(rng, monkeypatch, path, T, H, E, k):
+    """`auto` takes the size dispatch (one launch for decode-sized T, the
+    library GEMM + softmax/top-k kernel above it); `one_launch` forces the
+    single-kernel router at every size."""
     import mmfp4
+    from mmfp4 import moe_dispatch
+    if path == "one_launch":
+        monkeypatch.setattr(moe_dispatch, "_FUSED_ROUTER_MAX_T", 1 << 30)
+        monkeypatch.setattr(moe_dispatch, "_FUSED_ROUTER_MAX_WORK", 1 << 62)
     x = rng.normal(0, 1, (T, H)).astype(np.float16)
     w = (rng.normal(0, 1, (E, H)) / np.sqrt(H)).astype(np.float16)
     logits16 = (x.astype(np.float32) @ w.astype(np.float32).T).astype(np.float16)
@@ -57,7 +66,7 @@ def test_fused_router_vs_oracle(rng, T, H, E, k):
     gate = torch.nn.Linear(H, E, bias=False).to("cuda").half()
     with torch.no_grad():
         gate.weight.copy_(to_dev(w))
-    announce(f"fused router T={T} H={H} E={E} k={k}")
+    announce(f"fused router {path} T={T} H={H} E={E} k={k}")
     wts, ids = mmfp4.fused_router_topk(to_dev(x), gate, k)
     assert wts.dtype == torch.float16 and ids.dtype == torch.int64
     _check_topk(ids, wts.float(), ref, k, True)
