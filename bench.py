@@ -171,6 +171,36 @@ def run_prefill_bench(torch, mmfp4, M: int, steps: int, warmup: int):
             "launch_us_avg": 1e3 * total_ms / (steps * len(PREFILL))}
 
 
+def run_mfma_ceiling(torch, mmfp4, prefill_tflops: float):
+    """The sustained MFMA 32x32x16 f16 rate on this GPU with nothing else in
+    the loop (`mm_mfma_ceiling`), fed (a) the prefill GEMM's own operand
+    values -- N(0,1) fp16 activations and the decoded FP4 weights of the
+    config-4 matrices -- and (b) all-ones operands.  The board's power limit
+    lowers the clock as more operand bits toggle, so (a) is the practical
+    matrix-core ceiling of this GEMM and (b) shows the dense peak."""
+    from mmfp4 import _lib
+    n = 1 << 20
+    gen = torch.Generator(device="cuda").manual_seed(11)
+    acts = torch.randn(n, generator=gen, device="cuda").half()
+    wp, ws = make_weights(torch, mmfp4, 4096, 256, 13)
+    wdq = mmfp4.dequant_fp4(wp, ws, 4096, 256, G).reshape(-1).contiguous()
+    ones = torch.ones(n, device="cuda").half()
+    sink = torch.empty(256 * 512, dtype=torch.float32, device="cuda")
+    st = torch.cuda.current_stream().cuda_stream
+    iters = 400
+    flops = 256 * 8 * iters * 32 * 32768.0
+    res = {"kernel": "mm_mfma_ceiling (MFMA 32x32x16 f16 only, 256 blocks x 8 waves)"}
+    for name, a, b in (("gemm_operands", acts, wdq), ("ones", ones, ones)):
+        nh = min(a.numel(), b.numel()) // 8 * 8
+        fn = lambda a=a, b=b, nh=nh: _lib.call("mm_mfma_ceiling", a.data_ptr(), b.data_ptr(), nh,
+                                               iters, sink.data_ptr(), sink.numel() * 4, st)
+        ms = timed_launches(torch, [[fn]], 40, 40)
+        res[name + "_tflops"] = round(flops * 40 / (ms * 1e-3) / 1e12, 1)
+    res["prefill_fraction_of_gemm_operand_ceiling"] = round(
+        prefill_tflops / res["gemm_operands_tflops"], 4)
+    return res
+
+
 def run_single_bench(torch, mmfp4, M: int, K: int, N: int, steps: int):
     """One FP4 linear (config 1: M=1, 4096 -> 4096), rotated weight copies."""
     copies = max(2, -(-ROTATE_BYTES // alg_bytes(0, K, N)))
@@ -448,8 +478,9 @@ def main() -> int:
         elif args.section == "prefill":
             r = run_prefill_bench(torch, mmfp4, 2048, max(5, args.steps // 20),
                                   max(2, args.warmup // 10))
+            tf = r["flops"] / (r["ms_per_step"] * 1e-3) / 1e12
             res = {"ms_per_step": round(r["ms_per_step"], 4), "per_shape": r["per_shape"],
-                   "TFLOPs": round(r["flops"] / (r["ms_per_step"] * 1e-3) / 1e12, 1)}
+                   "TFLOPs": round(tf, 1), "mfma_ceiling": run_mfma_ceiling(torch, mmfp4, tf)}
         else:
             res = [run_moe_bench(torch, mmfp4, T, 20) for T in (32, 1024)]
         print(json.dumps({"section": args.section, "result": res}))
@@ -493,6 +524,7 @@ def main() -> int:
     out["config1_single_linear_m1"] = run_single_bench(torch, mmfp4, 1, 4096, 4096, 100)
     out["config5_moe_qwen3_30b_a3b"] = [run_moe_bench(torch, mmfp4, T, 20) for T in (32, 1024)]
     out["prefill_m2048"]["hipblaslt_fp16_same_shapes"] = hipblaslt_fp16_reference(torch, 2048)
+    out["prefill_m2048"]["mfma_ceiling"] = run_mfma_ceiling(torch, mmfp4, tflops)
     out["fused_next_rows"] = run_fused_bench(torch, mmfp4, 100)
     if True:   # the other BASELINE configs (2 at M=8/32, 3, 4 at M=512/8192), reported beside
         extra = {}

@@ -192,6 +192,16 @@ int mm_moe_mlp_fp4(const uint16_t* X, const void* expert_ids, int ids_i64, const
  * of the same size. */
 int mm_stream_read(const void* p, size_t bytes, uint32_t* sink, size_t sink_bytes, void* stream);
 
+/* Runs MFMA 32x32x16 f16 and nothing else on 256 blocks of 8 waves (one block
+ * per CU), with operand values taken from a and b (n_halves fp16 each, a
+ * multiple of 8, 16-byte aligned); sink receives 256 x 512 floats.  One launch
+ * performs 256 * 8 * iters * 32 MFMAs of 32768 flops.  No counterpart in the
+ * reference: a measurement aid for the sustained matrix-core rate with a
+ * GEMM's own operand values (the rate falls as more operand bits toggle,
+ * because the board's power limit lowers the clock). */
+int mm_mfma_ceiling(const uint16_t* a, const uint16_t* b, size_t n_halves, int iters, float* sink,
+                    size_t sink_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -45,6 +45,7 @@ SIGNATURES: dict[str, tuple] = {
     "mm_moe_mlp_fp4": (_c_int, [_vp, _vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_int, _c_int,
                                 _vp, _vp, _vp, _vp, _c_int, _vp, _vp, _vp, _vp, _vp]),
     "mm_stream_read": (_c_int, [_vp, _c_size, _vp, _c_size, _vp]),
+    "mm_mfma_ceiling": (_c_int, [_vp, _vp, _c_size, _c_int, _vp, _c_size, _vp]),
 }
 
 _lib = None

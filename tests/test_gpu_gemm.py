@@ -206,6 +206,27 @@ def test_stream_read_measurement_aid():
         _lib.call("mm_stream_read", buf.data_ptr(), 1000, sink.data_ptr(), sink.numel() * 4, st)
 
 
+def test_mfma_ceiling_measurement_aid():
+    """mm_mfma_ceiling's sums: with all-ones operands every accumulator gains
+    16 per MFMA and 4 MFMAs per iteration, and a lane's 8 accumulators add to
+    512 * iters; bad arguments are refused."""
+    from mmfp4 import _lib
+    ones = torch.ones(4096, dtype=torch.float16, device="cuda")
+    sink = torch.zeros(256 * 512, dtype=torch.float32, device="cuda")
+    st = torch.cuda.current_stream().cuda_stream
+    announce("mfma ceiling iters=3")
+    _lib.call("mm_mfma_ceiling", ones.data_ptr(), ones.data_ptr(), ones.numel(), 3,
+              sink.data_ptr(), sink.numel() * 4, st)
+    torch.cuda.synchronize()
+    assert torch.all(sink == 512 * 3)
+    with pytest.raises(ValueError):
+        _lib.call("mm_mfma_ceiling", ones.data_ptr(), ones.data_ptr(), 12, 3, sink.data_ptr(),
+                  sink.numel() * 4, st)
+    with pytest.raises(ValueError):
+        _lib.call("mm_mfma_ceiling", ones.data_ptr(), ones.data_ptr(), 4096, 3, sink.data_ptr(),
+                  1024, st)
+
+
 @pytest.mark.parametrize("M,K,N,g,int4", [(1, 512, 3072, 128, False), (8, 4160, 3076, 64, False),
                                           (3, 1024, 4096, 256, False), (5, 576, 6144, 64, False),
                                           (1, 1024, 3072, 128, True), (7, 640, 4100, 64, True),
