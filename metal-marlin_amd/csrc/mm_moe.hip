@@ -286,8 +286,12 @@ k_moe_prefill(const f16* __restrict__ X, const int32_t* __restrict__ sorted_idx,
   constexpr int SROWS = G64 ? PF2_SROWS_G64 : PF2_SROWS;
   using Sh = Pf2Shape<false, WM, WN, RB, CW, STAGES, SROWS>;
   constexpr int BM = Sh::BM, BN = Sh::BN;
-  __shared__ __attribute__((aligned(16))) char smem[Sh::LDS_BYTES];
-  __shared__ int tp[MOE_MAX_EXPERTS + 1];     // row-tile prefix over experts
+  // One LDS object only: with a second __shared__ array in the kernel the
+  // compiler cannot tell the operand reads from the in-flight global -> LDS
+  // copies and waits for all of them (vmcnt(0)) in every chunk, which
+  // serialises the load pipeline.  The row-tile prefix lives past the ring.
+  __shared__ __attribute__((aligned(16))) char smem[Sh::LDS_BYTES + (MOE_MAX_EXPERTS + 1) * 4];
+  int* const tp = (int*)(smem + Sh::LDS_BYTES);   // row-tile prefix over experts
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / WN, wn = wave % WN;
   const int l32 = lane & 31, h = lane >> 5;
