@@ -59,9 +59,15 @@ MM_DEV f16x8 raw_fp4_word(uint32_t w) {
 // (1024 + z) * sum(a), with sum(a) from one extra MFMA against a ones
 // operand.  The A operand is permuted to the same k order (a_k4_order).
 MM_DEV f16x8 u4_magic_word(uint32_t w) {
+  // (x & m) | (~m & c) is one v_bfi_b32 per pair; ~m & c == c here.  The
+  // mask passes through an empty asm (no instruction) into an SGPR so the
+  // compiler cannot fold ~m & c back to c -- with both constants literal it
+  // emits a separate and + or (a gfx9 VOP3 takes no literal operand).
+  uint32_t m = 0x000F000Fu;
+  asm("" : "+s"(m));
   u32x4 p;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) p[i] = ((w >> (4 * i)) & 0x000F000Fu) | 0x64006400u;
+  for (int i = 0; i < 4; ++i) p[i] = ((w >> (4 * i)) & m) | (~m & 0x64006400u);
   return __builtin_bit_cast(f16x8, p);
 }
 // (a0..a7) -> (a0, a4, a1, a5, a2, a6, a3, a7): the k order of u4_magic_word.
