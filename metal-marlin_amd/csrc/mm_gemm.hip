@@ -487,11 +487,11 @@ k_prefill2(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
   f32x16 acc[RB][CW];
   if constexpr (ACT == SK_PLAIN) {
     const DenseSrc src{A, lda, M, m0, N, n0, B, S, Z, N};
-    pf2_mainloop<INT4, WM, WN, RB, CW, G64, false, PF2_STAGES, SROWS>(src, K, g, c_beg, c_end, RB,
-                                                                   smem, acc);
+    pf2_mainloop<INT4, WM, WN, RB, CW, G64, false, PF2_STAGES, SROWS>(src, K, g, c_beg, c_end,
+                                                                  smem, acc);
   } else {
     const PairSrc src{A, lda, M, m0, N, n0, B, B2, S, S2, Z, Z2, N};
-    pf2_mainloop<INT4, WM, WN, RB, CW, G64, true, PF2_STAGES, SROWS>(src, K, g, c_beg, c_end, RB,
+    pf2_mainloop<INT4, WM, WN, RB, CW, G64, true, PF2_STAGES, SROWS>(src, K, g, c_beg, c_end,
                                                                   smem, acc);
   }
 

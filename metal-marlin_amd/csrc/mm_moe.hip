@@ -341,8 +341,16 @@ k_moe_prefill(const f16* __restrict__ X, const int32_t* __restrict__ sorted_idx,
   const int rb_live =
       __builtin_amdgcn_readfirstlane(min(RB, max(0, (rows - wm * 32 * RB + 31) / 32)));
   f32x16 acc[RB][CW];
-  pf2_mainloop<false, WM, WN, RB, CW, G64, true, STAGES, SROWS>(src, K, g, 0, K / PF2_BK, rb_live,
-                                                                smem, acc);
+  // The live row-block count is wave-uniform and fixed for the tile: one
+  // switch here keeps the main loop free of per-step branches.
+  static_for(
+      [&](auto lc) {
+        constexpr int L = decltype(lc)::value;
+        if (rb_live == L)
+          pf2_mainloop<false, WM, WN, RB, CW, G64, true, STAGES, SROWS, L>(src, K, g, 0,
+                                                                           K / PF2_BK, smem, acc);
+      },
+      std::make_integer_sequence<int, RB + 1>{});
 
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {

@@ -102,12 +102,17 @@ struct Pf2Shape {
 //                       consecutive columns starting at P (clamped in range);
 //   src.scol(P, w), src.zcol(P, w) -> const f16*, the same for scales / zeros;
 //   src.ld           -> row stride of B in words and of S/Z in halves.
-// rb_live: the wave's row blocks past it hold no valid row and skip their
-// MFMAs (wave-uniform).  Requires K % 64 == 0.
+// RBL: the wave's row blocks from RBL on hold no valid row; they skip their
+// A reads and MFMAs (acc[RBL..RB) stays zero).  A compile-time count, so no
+// branch splits the MFMA stream from the interleaved LDS reads and decode;
+// callers with a per-wave count switch over it once, outside the loop.  The
+// wave still issues its share of the loads and joins every barrier.
+// Requires K % 64 == 0.
 template <bool INT4, int WM, int WN, int RB, int CW, bool G64, bool TM, int STAGES, int SROWS,
-          class Src>
-MM_DEV void pf2_mainloop(const Src& src, int K, int g, int c_beg, int c_end, int rb_live,
-                         char* smem, f32x16 (&acc)[RB][CW]) {
+          int RBL = RB, class Src>
+MM_DEV void pf2_mainloop(const Src& src, int K, int g, int c_beg, int c_end, char* smem,
+                         f32x16 (&acc)[RB][CW]) {
+  static_assert(RBL >= 0 && RBL <= RB, "live row blocks");
   static_assert(G64 || SROWS >= PF2_SROWS, "a chunk can touch 8 groups unless g % 64 == 0");
   using Sh = Pf2Shape<INT4, WM, WN, RB, CW, STAGES, SROWS>;
   constexpr int NWAVE = Sh::NWAVE, BN = Sh::BN;
@@ -219,6 +224,7 @@ MM_DEV void pf2_mainloop(const Src& src, int K, int g, int c_beg, int c_end, int
     wait_vmcnt<(STAGES - 2) * Sh::LOADS_PER_CHUNK>();
     __builtin_amdgcn_s_barrier();
     issue(min(ch + STAGES - 1, nch - 1), (st + STAGES - 1) % STAGES);
+    if constexpr (RBL == 0) return;   // no live rows: loads and barriers only
     const int k0 = ch * PF2_BK;
     const int gi0 = k0 / g;
     f16x8 af[2][RB];
@@ -246,7 +252,7 @@ MM_DEV void pf2_mainloop(const Src& src, int K, int g, int c_beg, int c_end, int
         if constexpr (INT4) zv[slot] = read_s(Z_OFF + st * S_BYTES + so);
       }
 #pragma unroll
-      for (int rb = 0; rb < RB; ++rb)
+      for (int rb = 0; rb < RBL; ++rb)
         af[slot][rb] = *(const f16x8*)(smem + a_off[t] + st * A_BYTES + rb * 32 * 128);
     };
     auto decode = [&](int slot, f16x8 (&b)[CW]) {
@@ -273,12 +279,11 @@ MM_DEV void pf2_mainloop(const Src& src, int K, int g, int c_beg, int c_end, int
       const int cur = t & 1;
       if (t + 1 < PF2_BK / 16) frag(t + 1, cur ^ 1);
 #pragma unroll
-      for (int rb = 0; rb < RB; ++rb)
-        if (rb < rb_live)
+      for (int rb = 0; rb < RBL; ++rb)
 #pragma unroll
-          for (int j = 0; j < CW; ++j)
-            acc[rb][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[cur][rb], bq[cur][j],
-                                                                acc[rb][j], 0, 0, 0);
+        for (int j = 0; j < CW; ++j)
+          acc[rb][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[cur][rb], bq[cur][j],
+                                                              acc[rb][j], 0, 0, 0);
       if (t + 1 < PF2_BK / 16) decode(cur ^ 1, bq[cur ^ 1]);
       // Interleave each MFMA with a share of the next step's LDS reads and
       // decode VALU so the matrix pipe never drains while they issue.  Up to
@@ -286,7 +291,7 @@ MM_DEV void pf2_mainloop(const Src& src, int K, int g, int c_beg, int c_end, int
       // step's operands) measured 2-6% faster than 1 and 3 at M = 512..8192.
 #if MM_PF2_SCHED > 0
 #pragma unroll
-      for (int i = 0; i < RB * CW; ++i) {
+      for (int i = 0; i < RBL * CW; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
         __builtin_amdgcn_sched_group_barrier(0x100, MM_PF2_SCHED_DS, 0);   // DS read
         __builtin_amdgcn_sched_group_barrier(0x002, MM_PF2_SCHED_VALU, 0);   // VALU
