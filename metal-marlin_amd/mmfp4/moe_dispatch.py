@@ -133,9 +133,7 @@ def _router(hidden: torch.Tensor, weight_eh: torch.Tensor, bias: torch.Tensor | 
     if T > _FUSED_ROUTER_MAX_T or T * H * E > _FUSED_ROUTER_MAX_WORK:
         w16 = weight_eh.to(torch.float16).contiguous()
         b16 = None if bias is None else bias.to(torch.float16)
-        logits = torch.nn.functional.linear(x, w16, b16)
-        p, ids = router_softmax_topk(logits, top_k, renormalize)
-        return p.to(torch.float32), ids
+        return _softmax_topk(torch.nn.functional.linear(x, w16, b16), top_k, renormalize)
     w = _half(weight_eh)
     b = None if bias is None else bias.to(torch.float32).contiguous()
     ids = torch.empty((T, top_k), dtype=torch.int64, device=dev)
@@ -168,11 +166,8 @@ def fused_router_topk(hidden_states: torch.Tensor, gate: nn.Linear, top_k: int,
     return probs.to(gate.weight.dtype), ids
 
 
-def router_softmax_topk(gate_logits: torch.Tensor, top_k: int, renormalize: bool = True):
-    """fp32 softmax -> top-k (descending) -> optional renormalisation of given
-    logits [T, E] in one launch (moe_dispatch.py:99-151,
-    _router_softmax_fusion).  Returns (topk_probs in the logits' dtype,
-    topk_indices int64)."""
+def _softmax_topk(gate_logits: torch.Tensor, top_k: int, renormalize: bool):
+    """mm_softmax_topk over logits [..., E] -> (probs fp32 [T, k], ids int64 [T, k])."""
     dev = _lib.require_device(gate_logits)
     E = gate_logits.shape[-1]
     lg = gate_logits.reshape(-1, E)
@@ -183,6 +178,15 @@ def router_softmax_topk(gate_logits: torch.Tensor, top_k: int, renormalize: bool
     probs = torch.empty((T, top_k), dtype=torch.float32, device=dev)
     _lib.call("mm_softmax_topk", _lib.ptr(lg), int(f32), T, E, top_k, int(renormalize),
               _lib.ptr(ids), _lib.ptr(probs), _lib.stream_of(lg))
+    return probs, ids
+
+
+def router_softmax_topk(gate_logits: torch.Tensor, top_k: int, renormalize: bool = True):
+    """fp32 softmax -> top-k (descending) -> optional renormalisation of given
+    logits [T, E] in one launch (moe_dispatch.py:99-151,
+    _router_softmax_fusion).  Returns (topk_probs in the logits' dtype,
+    topk_indices int64)."""
+    probs, ids = _softmax_topk(gate_logits, top_k, renormalize)
     lead = tuple(gate_logits.shape[:-1])
     return probs.to(gate_logits.dtype).reshape(*lead, top_k), ids.reshape(*lead, top_k)
 
