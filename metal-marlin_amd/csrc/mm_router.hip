@@ -257,18 +257,18 @@ MM_DEV float row_sum(float v) {
   return v + dpp_f<DPP_MIRROR>(v);
 }
 
-template <int SL>
-MM_DEV void softmax_topk_rows16(const float* lg, int rstride, int nvalid, int E, int k, int renorm,
-                                int64_t* ids, float* probs) {
+// ld(j, e): logit e of row j (e < E).
+template <int SL, class Ld>
+MM_DEV void softmax_topk_rows16(Ld ld, int nvalid, int E, int k, int renorm, int64_t* ids,
+                                float* probs) {
   const int lane = threadIdx.x & 63;
   const int j = lane >> 4, l = lane & 15;
-  const float* row = lg + j * rstride;
   float p[SL];
   float mx = -INFINITY;
 #pragma unroll
   for (int sl = 0; sl < SL; ++sl) {
     const int e = l + 16 * sl;
-    p[sl] = e < E ? row[e] : -INFINITY;
+    p[sl] = e < E ? ld(j, e) : -INFINITY;
     mx = fmaxf(mx, p[sl]);
   }
   mx = row_max(mx);
@@ -433,8 +433,9 @@ k_moe_router(const f16* __restrict__ X, const f16* __restrict__ W, const float* 
   const int r0 = wave * NR;
   if (t0 + r0 < T) {
     if constexpr (R16)
-      softmax_topk_rows16<SL>(lg + r0 * E, E, min(NR, T - t0 - r0), E, k, renorm,
-                              ids + (size_t)(t0 + r0) * k, probs + (size_t)(t0 + r0) * k);
+      softmax_topk_rows16<SL>([&](int j, int e) { return lg[(r0 + j) * E + e]; },
+                              min(NR, T - t0 - r0), E, k, renorm, ids + (size_t)(t0 + r0) * k,
+                              probs + (size_t)(t0 + r0) * k);
     else
       softmax_topk_rows<NR, SL>(lg + r0 * E, E, min(NR, T - t0 - r0), E, k, renorm,
                                 ids + (size_t)(t0 + r0) * k, probs + (size_t)(t0 + r0) * k);
@@ -469,6 +470,23 @@ k_softmax_topk(const void* __restrict__ logits, int logits_f32, int T, int E, in
   const int t0 = (blockIdx.x * RT_WAVES + wave) * NR;
   if (t0 >= T) return;
   const int nv = min(NR, T - t0);
+  if constexpr (R16) {
+    // 16 lanes per row: each lane loads its own logits, no LDS staging.
+    // Rows past T read the last row (their results are not stored).
+    const size_t base = (size_t)t0 * E;
+    const int jmax = nv - 1;
+    if (logits_f32)
+      softmax_topk_rows16<SL>(
+          [&](int j, int e) { return ((const float*)logits)[base + (size_t)min(j, jmax) * E + e]; },
+          nv, E, k, renorm, ids + (size_t)t0 * k, probs + (size_t)t0 * k);
+    else
+      softmax_topk_rows16<SL>(
+          [&](int j, int e) {
+            return (float)((const f16*)logits)[base + (size_t)min(j, jmax) * E + e];
+          },
+          nv, E, k, renorm, ids + (size_t)t0 * k, probs + (size_t)t0 * k);
+    return;
+  }
   float* rows = lg + (size_t)wave * NR * E;
   for (int j = 0; j < nv; ++j)
     for (int e = lane; e < E; e += 64)
@@ -476,9 +494,6 @@ k_softmax_topk(const void* __restrict__ logits, int logits_f32, int T, int E, in
                                    : (float)((const f16*)logits)[(size_t)(t0 + j) * E + e];
   if constexpr (SL == 0) {
     softmax_topk_row(rows, E, k, renorm, ids + (size_t)t0 * k, probs + (size_t)t0 * k);
-  } else if constexpr (R16) {
-    softmax_topk_rows16<SL>(rows, E, nv, E, k, renorm, ids + (size_t)t0 * k,
-                            probs + (size_t)t0 * k);
   } else {
     softmax_topk_rows<NR, SL>(rows, E, nv, E, k, renorm, ids + (size_t)t0 * k,
                               probs + (size_t)t0 * k);
@@ -545,7 +560,8 @@ extern "C" int mm_softmax_topk(const void* logits, int logits_f32, int T, int E,
   if (T == 0) return 0;
   const int sl = rt_slots(E), sl16 = rt16_slots(E);
   const int nr = sl == 0 ? 1 : 4;               // tokens per wave
-  const size_t lds = (size_t)RT_WAVES * nr * E * sizeof(float);
+  // The 16-lanes-per-row layout (sl16 > 0) reads the logits into registers.
+  const size_t lds = sl16 > 0 ? 0 : (size_t)RT_WAVES * nr * E * sizeof(float);
   const dim3 grid(mm_cdiv(T, RT_WAVES * nr));
 #define MM_LAUNCH_ST(NRV, SLV, R16)                                                              \
   hipLaunchKernelGGL((k_softmax_topk<NRV, SLV, R16>), grid, dim3(RT_WAVES * 64), lds,             \
