@@ -187,7 +187,8 @@ def test_gpu_grouping_api(rng, T, k, E):
 
 
 @pytest.mark.parametrize("E,T,k,H,I,i64", [(128, 32, 8, 2048, 768, True), (16, 1, 4, 256, 128, False),
-                                          (64, 256, 8, 512, 256, True), (8, 3, 8, 256, 128, False)])
+                                          (64, 256, 8, 512, 256, True), (8, 3, 8, 256, 128, False),
+                                          (1, 4, 1, 384, 128, False), (128, 5, 8, 2048, 768, False)])
 def test_moe_mlp_one_call_matches_steps(rng, E, T, k, H, I, i64):
     """mm_moe_mlp_fp4 (one library call) is bit-identical to the sort ->
     grouped GEMM -> grouped GEMM -> combine steps on the same inputs."""
@@ -207,3 +208,29 @@ def test_moe_mlp_one_call_matches_steps(rng, E, T, k, H, I, i64):
     y = md._grouped(a, s_idx, offs, False, k, T, to_dev(DP), to_dev(DS), g, 0)
     ref = md.scatter_expert_outputs(y, dp, md.MoEDispatchInfo(s_idx, s_idx, offs, inv, T, k, E, s_idx))
     assert torch.equal(fused, ref)
+
+
+def test_moe_mlp_back_to_back_calls(rng):
+    """Decode-sized calls form the output in the down launch (last block per
+    128 columns, arrival counters cleared by the sort): consecutive calls of
+    different sizes on one stream each match their step-by-step result."""
+    import mmfp4
+    from mmfp4 import moe_dispatch as md
+    E, H, I, k, g = 32, 512, 256, 4, 128
+    GU, GS = _experts(rng, E, H, 2 * I, g)
+    DP, DS = _experts(rng, E, I, H, g)
+    dGU, dGS, dDP, dDS = to_dev(GU), to_dev(GS), to_dev(DP), to_dev(DS)
+    outs, refs = [], []
+    for T in (16, 3, 16, 1):
+        x = to_dev(rng.normal(0, 1, (T, H)).astype(np.float16))
+        ids, probs = omoe.router_topk(rng.normal(0, 1, (T, E)).astype(np.float32), k)
+        dids, dp = to_dev(ids.astype(np.int32)), to_dev(probs)
+        announce(f"moe mlp back-to-back T={T}")
+        outs.append(mmfp4.moe_mlp_fp4(x, dGU, dGS, dDP, dDS, dids, dp, g))
+        s_idx, offs, inv = md._sort(dids, E)
+        a = md._grouped(x, s_idx, offs, True, k, T, dGU, dGS, g, 1)
+        y = md._grouped(a, s_idx, offs, False, k, T, dDP, dDS, g, 0)
+        refs.append(md.scatter_expert_outputs(
+            y, dp, md.MoEDispatchInfo(s_idx, s_idx, offs, inv, T, k, E, s_idx)))
+    for o, r in zip(outs, refs):
+        assert torch.equal(o, r)
