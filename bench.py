@@ -384,7 +384,9 @@ def cpu_baseline(budget_s: float = 15.0):
         for a, p, s in mats:
             marlin_gemm_fp4_cpu(a, p, s, G)
         steps += 1
-        if time.perf_counter() - t0 > budget_s or steps >= 10:
+        elapsed = time.perf_counter() - t0
+        # a bounded sample of at least ~10 s of CPU work (and at least 3 steps)
+        if (elapsed >= 10.0 and steps >= 3) or elapsed > budget_s:
             break
     dt = (time.perf_counter() - t0) / steps
     step_bytes = sum(alg_bytes(1, K, N) for _, K, N in LLAMA_LAYER)
