@@ -686,6 +686,12 @@ int launch_skinny(const f16* A, int lda, const uint32_t* B, const f16* S, const 
 #ifndef MM_SK_DUAL_NW
 #define MM_SK_DUAL_NW 8
 #endif
+// 64-k steps per wave per round.  Measured at M=1 (qkv / o): 8 waves x 8
+// steps 5.51 / 5.25 us, 8 x 4 5.46 / 5.12, 16 x 4 5.89 / 5.54, 4 x 8
+// 6.12 / 5.79, 4 x 16 5.99 / 5.69.
+#ifndef MM_SK_DUAL_SPW
+#define MM_SK_DUAL_SPW MM_SK_SPW1
+#endif
 // The two-slab kernel serves M <= 8 layers whose 64-column plan runs unsplit
 // on fewer than MM_SK_DUAL_BELOW blocks, when 32-column tiles give at least
 // MM_SK_DUAL_MIN_TILES blocks (measured on MI355X at M=1: 4096 -> 6144
@@ -702,7 +708,7 @@ int launch_skinny(const f16* A, int lda, const uint32_t* B, const f16* S, const 
 
 bool use_dual(int M, int N, int K, int g) {
   if (!MM_SK_DUAL || M > 8 || K % 64 != 0 || g % 64 != 0 || N % 4 != 0) return false;
-  if (flush_steps(g / 2, sk_spw<1>()) == 0) return false;
+  if (flush_steps(g / 2, MM_SK_DUAL_SPW) == 0) return false;
   return (plan_skinny(M, N, K).ksplit == 1 || (MM_SK_DUAL_SMALL && (long)K * N <= 4096L * 4096)) &&
          mm_cdiv(N, SK_COLS) < MM_SK_DUAL_BELOW && mm_cdiv(N, 32) >= MM_SK_DUAL_MIN_TILES;
 }
@@ -710,7 +716,7 @@ bool use_dual(int M, int N, int K, int g) {
 template <bool INT4>
 int launch_dual(const f16* A, const uint32_t* B, const f16* S, const f16* Z, f16* C, int M, int N,
                 int K, int g, hipStream_t st) {
-  constexpr int SPW = sk_spw<1>(), NW = MM_SK_DUAL_NW;
+  constexpr int SPW = MM_SK_DUAL_SPW, NW = MM_SK_DUAL_NW;
   const int nsteps = K / 64;                           // 64-k steps
   const int nrounds = mm_cdiv(nsteps, NW * SPW);
   const int fl = flush_steps(g / 2, SPW);              // 64-k steps per scale group
