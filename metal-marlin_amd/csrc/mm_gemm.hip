@@ -793,6 +793,9 @@ int launch_prefill(const f16* A, int lda, const uint32_t* B, const f16* S, const
 #define PF2_SMALL 1, 4, 2, 2     // 64 x 256, 4 waves of 64 x 64
 #endif
 
+#ifndef MM_PF_KS_BLOCKS
+#define MM_PF_KS_BLOCKS 200   // split K while the grid has fewer blocks than this
+#endif
 // Prefill plan: tile config (0: 256x256, 1: 128x256, 2: 64x256) and K split.
 struct PrefillPlan {
   int cfg;
@@ -809,7 +812,7 @@ PrefillPlan plan_prefill(int M, int N, int K) {
   // chunks of 64 k so the pipeline stays full.
   const int nch = K / PF2_BK;
   int ks = 1;
-  while (blocks * ks < 200 && nch / (ks * 2) >= 8) ks *= 2;
+  while (blocks * ks < MM_PF_KS_BLOCKS && nch / (ks * 2) >= 8) ks *= 2;
   p.ksplit = ks;
   return p;
 }
