@@ -223,9 +223,10 @@ def rand_weights(torch, K: int, N: int, gen):
 
 
 def run_fused_bench(torch, mmfp4, steps: int):
-    """SURVEY next rows at the Llama-3-8B shapes, fused vs unfused, rotated
-    weight copies: gate_up+SiLU (4096 -> 2 x 14336) at M=1 and M=2048, and
-    the Q/K/V projections (4096 -> 4096 + 1024 + 1024) at M=1."""
+    """The operators either side of the GEMM at the Llama-3-8B and Qwen3 MoE
+    shapes, fused vs unfused, rotated weight copies: gate_up+SiLU (4096 ->
+    2 x 14336) at M=1 and M=2048, the Q/K/V projections (4096 -> 4096 + 1024
+    + 1024) at M=1, and the router at T=32 and T=1024."""
     gen = torch.Generator(device="cuda").manual_seed(900)
     res = {}
     K, N = 4096, 14336
@@ -458,8 +459,8 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only: the FP4 dequant-GEMM "
-                          "path is single-GPU by design (see DESIGN.md for how it would "
-                          "shard); run with --gpus 1"}))
+                          "path runs on a single GPU (column- or expert-sharded multi-GPU "
+                          "runs are not part of it); run with --gpus 1"}))
         return 2
 
     import torch
