@@ -306,6 +306,9 @@ def dequantize_mmfp4(packed: torch.Tensor, scales: torch.Tensor,
 
 
 def select_decode_kernel(M: int, N: int, K: int) -> str:
-    """Kernel family the library runs for an M x K x N problem (the
-    reference's selector is kernels_core.py:3833-3852)."""
-    return "decode_gemv_fp4" if M <= 32 else "marlin_gemm_fp4"
+    """Kernel-family recommendation of kernels_core.py:3833-3852, same rule
+    and names: "marlin_gemm_fp4" for M > 8, else "decode_gemv_fp4".  (The
+    library chooses its own kernel inside mm_fp4_gemm: the skinny decode
+    kernels up to M = 32, the MFMA tile kernel above.)"""
+    del N, K
+    return "marlin_gemm_fp4" if M > 8 else "decode_gemv_fp4"
