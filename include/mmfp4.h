@@ -72,6 +72,17 @@ size_t mm_gemm_workspace_bytes(int M, int N, int K);
 int mm_fp4_gemm(const uint16_t* A, const uint32_t* B, const uint16_t* scales, uint16_t* C, int M,
                 int N, int K, int group_size, void* ws, size_t ws_bytes, void* stream);
 
+/* C[M,N] = A[M,K] . dequant_fp4(B, scales)^T for row-packed (MMFP4) weights:
+ * B [N, K/8] uint32 (word (n, kp) holds k = 8kp .. 8kp+7 of row n), scales
+ * fp16 [N, K/g].  Decode sizes only: M <= 16, K % 256 == 0, g % 64 == 0,
+ * N % 4 == 0; the weights are read in place (no transpose).  Workspace as
+ * mm_gemm_workspace_bytes(M, N, K).  Replaces metal_marlin/layers/
+ * mmfp4_linear.py:549-598 (mmfp4_gemm), which transposes the row-packed
+ * words to the [K/8, N] layout on every call (:414-478). */
+int mm_fp4_gemm_rowpacked(const uint16_t* A, const uint32_t* B, const uint16_t* scales,
+                          uint16_t* C, int M, int N, int K, int group_size, void* ws,
+                          size_t ws_bytes, void* stream);
+
 /* INT4 asymmetric counterpart.  Replaces metal_marlin/kernels_core.py:1959-2066
  * (marlin_gemm_int4) and metal_marlin/metal_dispatch.py:1863-1937
  * (MetalKernelLibrary.int4_gemm). */

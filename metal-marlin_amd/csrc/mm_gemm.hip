@@ -60,7 +60,7 @@ struct SkMulti {
 // SK_PAIR (NT = 2): tile 0 is columns [n0, n0+64) of (B, S, Z) and tile 1
 // the same columns of (B2, S2, Z2).  Split-K partials are [ksplit][M][PW]
 // fp32 with PW = N, 2N for the pair modes (gate at n, up at N + n), or ntot.
-template <bool INT4, int MT, int NT, int SPW, int NW, int FL, int ACT>
+template <bool INT4, int MT, int NT, int SPW, int NW, int FL, int ACT, bool ROWP = false>
 __global__ void __launch_bounds__(NW * 64)
 k_skinny(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
          const f16* __restrict__ S, const f16* __restrict__ Z, const uint32_t* __restrict__ B2,
@@ -109,8 +109,14 @@ k_skinny(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
   for (int t = 0; t < NT; ++t)
     tl[t] = ONE ? SkTile{B, S, Z, n0 + t * SK_COLS}
                 : (t == 0 ? SkTile{B, S, Z, n0} : SkTile{B2, S2, Z2, n0});
-  skinny_wave<INT4, MT, NT, SPW, FL>(A, lda, nullptr, 1, M, tl, N, K, g, blk_st0 + wave * SPW,
-                                     nrounds, NW * SPW, acc);
+  if constexpr (ROWP) {
+    // Row-packed weights ([N, K/8] words, [N, K/g] scales): FP4, one tile.
+    static_assert(!INT4 && NT == 1 && ACT == SK_PLAIN, "row-packed: plain FP4 product");
+    rowp_wave<MT, SPW>(A, lda, M, tl[0], N, K, g, blk_st0 + wave * SPW, nrounds, NW * SPW, acc);
+  } else {
+    skinny_wave<INT4, MT, NT, SPW, FL>(A, lda, nullptr, 1, M, tl, N, K, g, blk_st0 + wave * SPW,
+                                       nrounds, NW * SPW, acc);
+  }
   skinny_block_reduce<MT, NT, NW>(red, acc, M);
 
   // Lane (c, q) of wave 0 holds rows 16*mt + 4*q + rr, columns 4*c + j of
@@ -638,7 +644,7 @@ size_t skinny_ws_bytes(int M, int N, int K) {
 // B2/S2/Z2 the up matrix, both [.., N]; the split and workspace are those of
 // the unfused [K, 2N] product (plan_skinny(M, 2N, K)).
 // SK_MULTI: `mp` describes the matrices (N is then mp->ntot, B..Z2 unused).
-template <bool INT4, int MT, int ACT>
+template <bool INT4, int MT, int ACT, bool ROWP = false>
 int launch_skinny(const f16* A, int lda, const uint32_t* B, const f16* S, const f16* Z,
                   const uint32_t* B2, const f16* S2, const f16* Z2, f16* C, int ldc, int M,
                   int N, int K, int g, void* ws, size_t ws_bytes, hipStream_t st,
@@ -662,15 +668,19 @@ int launch_skinny(const f16* A, int lda, const uint32_t* B, const f16* S, const 
   constexpr int SPW = sk_spw<MT>();
   const int fl = flush_steps(g, SPW);
 #define MM_LAUNCH_SK(FLV)                                                                   \
-  hipLaunchKernelGGL((k_skinny<INT4, MT, NT, SPW, sk_nw<MT>(), FLV, ACT>), grid, dim3(sk_nw<MT>() * 64), 0, \
+  hipLaunchKernelGGL((k_skinny<INT4, MT, NT, SPW, sk_nw<MT>(), FLV, ACT, ROWP>), grid, dim3(sk_nw<MT>() * 64), 0, \
                      st, A, lda, B, S, Z, B2, S2, Z2, C, ldc, M, N, K, g, p.nrounds, part,       \
                      counters, mp ? *mp : none)
-  switch (fl) {
-    case 1: MM_LAUNCH_SK(1); break;
-    case 2: MM_LAUNCH_SK(2); break;
-    case 4: MM_LAUNCH_SK(4 <= SPW ? 4 : 0); break;
-    case 8: MM_LAUNCH_SK(8 <= SPW ? 8 : 0); break;
-    default: MM_LAUNCH_SK(0); break;
+  if constexpr (ROWP) {
+    MM_LAUNCH_SK(0);   // pre-scale: rowp_wave applies each lane's own group scale
+  } else {
+    switch (fl) {
+      case 1: MM_LAUNCH_SK(1); break;
+      case 2: MM_LAUNCH_SK(2); break;
+      case 4: MM_LAUNCH_SK(4 <= SPW ? 4 : 0); break;
+      case 8: MM_LAUNCH_SK(8 <= SPW ? 8 : 0); break;
+      default: MM_LAUNCH_SK(0); break;
+    }
   }
 #undef MM_LAUNCH_SK
   MM_CHECK_LAUNCH("gemm(skinny)");
@@ -1027,6 +1037,28 @@ extern "C" int mm_fp4_gemm(const uint16_t* A, const uint32_t* B, const uint16_t*
                            int M, int N, int K, int g, void* ws, size_t ws_bytes, void* stream) {
   return gemm_dispatch<false>("mm_fp4_gemm", (const f16*)A, B, (const f16*)S, nullptr, (f16*)C, M,
                               N, K, g, ws, ws_bytes, (hipStream_t)stream);
+}
+
+extern "C" int mm_fp4_gemm_rowpacked(const uint16_t* A, const uint32_t* B, const uint16_t* S,
+                                     uint16_t* C, int M, int N, int K, int g, void* ws,
+                                     size_t ws_bytes, void* stream) {
+  const char* who = "mm_fp4_gemm_rowpacked";
+  MM_CHECK_ARG(M >= 0 && N > 0 && K > 0, "%s: bad shape M=%d N=%d K=%d", who, M, N, K);
+  MM_CHECK_ARG(M <= 16, "%s: M=%d: the row-packed decode kernel takes M <= 16 (larger M: "
+               "transpose to the [K/8, N] layout and call mm_fp4_gemm)", who, M);
+  MM_CHECK_ARG(K % 256 == 0, "%s: K=%d must be divisible by 256", who, K);
+  MM_CHECK_ARG(g > 0 && g % 64 == 0 && K % g == 0,
+               "%s: group_size=%d must be a multiple of 64 dividing K=%d", who, g, K);
+  MM_CHECK_ARG(N % 4 == 0, "%s: N=%d must be divisible by 4", who, N);
+  MM_CHECK_ARG((size_t)N * (size_t)(K / 8) * 4 < ((size_t)1 << 32),
+               "%s: the packed weights must be under 4 GiB", who);
+  MM_CHECK_ARG(((uintptr_t)A & 15) == 0 && ((uintptr_t)B & 15) == 0 && ((uintptr_t)S & 1) == 0 &&
+                   ((uintptr_t)C & 7) == 0,
+               "%s: A and the packed weights must be 16-byte aligned, C 8-byte", who);
+  if (M == 0) return 0;
+  return launch_skinny<false, 1, SK_PLAIN, true>((const f16*)A, K, B, (const f16*)S, nullptr,
+                                                 nullptr, nullptr, nullptr, (f16*)C, N, M, N, K,
+                                                 g, ws, ws_bytes, (hipStream_t)stream);
 }
 
 extern "C" int mm_u4_gemm(const uint16_t* A, const uint32_t* B, const uint16_t* S,

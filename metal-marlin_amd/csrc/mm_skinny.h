@@ -252,6 +252,67 @@ MM_DEV void skinny_wave(const f16* __restrict__ A, int lda, const int* __restric
   }
 }
 
+// skinny_wave for row-packed FP4 weights (MMFP4 layout): B [N, K/8] words
+// (word (n, kp) holds k = 8kp .. 8kp+7 of column n, LSB-first nibbles) and
+// scales [N, K/g].  The MFMA only needs the activation and weight operands to
+// agree on the k order, so lane (c, q) takes, in a round of SPW 32-k steps
+// (word rows 4*stb .. 4*stb + 4*SPW), the contiguous rows
+// kp(i) = 4*stb + q*SPW + i for step i: each of its four columns is then read
+// as SPW/4 16-byte vectors, the same load count as the Marlin-layout core.
+// (Measured on MI355X, this order beats giving the four lanes q of a column
+// 64 contiguous bytes per load: 4096x28672 at M=1 21.6 vs 25.5 us.)  The
+// eight rows of a lane lie in one scale group (g % 64 == 0), but the lanes q
+// of an MFMA can straddle a group, so weights are scaled before the MFMA
+// (pre-scale, bit-exact fp16 values).  Requires K % 256 == 0 (every round lies
+// inside K) and SPW == 8.
+template <int MT, int SPW>
+MM_DEV void rowp_wave(const f16* __restrict__ A, int lda, int M, const SkTile& tl, int N, int K,
+                      int g, int st0, int nrounds, int ststride, f32x4 (&acc)[MT][1][4]) {
+  static_assert(SPW == 8, "a lane's run of rows is one 64-k piece of a scale group");
+  const int lane = threadIdx.x & 63;
+  const int c = lane & 15, q = lane >> 4;
+  const int KP = K >> 3, G = K / g;
+  const int nsteps = KP >> 2;                 // K % 256 == 0: whole steps and rounds
+  uint32_t aoff[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) aoff[mt] = (uint32_t)min(mt * 16 + c, M - 1) * (uint32_t)lda * 2u;
+  const uint32_t col = (uint32_t)min(tl.col0 + 4 * c, N - 4);   // lane's first column
+  st0 = __builtin_amdgcn_readfirstlane(st0);
+  for (int r = 0; r < nrounds; ++r) {
+    const int stb = st0 + r * ststride;
+    if (stb >= nsteps) break;
+    const uint32_t kp0 = (uint32_t)(4 * stb + q * SPW);        // lane's first word row
+    const uint32_t gi = kp0 * 8u / (uint32_t)g;
+    f16 sc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      sc[j] = sanitize_scale(*at_bytes<f16>(tl.S, ((col + j) * (uint32_t)G + gi) * 2u));
+    u32x4 w[4][SPW / 4];                                        // [column][4 rows]
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int u = 0; u < SPW / 4; ++u) {
+        const uint32_t off = ((col + j) * (uint32_t)KP + kp0 + 4u * u) * 4u;
+        w[j][u] = MM_SK_NT ? __builtin_nontemporal_load(at_bytes<u32x4>(tl.B, off))
+                           : *at_bytes<u32x4>(tl.B, off);
+      }
+    f16x8 a[SPW][MT];
+#pragma unroll
+    for (int i = 0; i < SPW; ++i)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) a[i][mt] = *at_bytes<f16x8>(A, aoff[mt] + (kp0 + i) * 16u);
+#pragma unroll
+    for (int i = 0; i < SPW; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const f16x8 b = WordDq<false>::run(w[j][i >> 2][i & 3], sc[j], (f16)0);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+          acc[mt][0][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i][mt], b, acc[mt][0][j], 0, 0, 0);
+      }
+  }
+}
+
 // Every wave but wave 0 parks its accumulators in LDS ((NW-1) tiles), one
 // barrier, then wave 0 adds them in wave order (deterministic).  On return
 // wave 0 holds the block sum; the other waves' values are unspecified.

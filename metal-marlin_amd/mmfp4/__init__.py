@@ -7,7 +7,8 @@ from .kernels import (FP4_PER_UINT, decode_gemv_fp4, dequant_fp4, dequant_fp4_de
                       marlin_gemm_fp4_tuned, marlin_gemm_fused_fp4, marlin_gemm_fused_u4,
                       marlin_gemm_int4, mmfp4_fused_gate_up, mmfp4_fused_gate_up_marlin,
                       mmfp4_fused_qkv,
-                      mmfp4_gemm, select_decode_kernel)
+                      mmfp4_gemm, mmfp4_gemm_rowpacked, rowpacked_gemm_supported,
+                      select_decode_kernel)
 from .gpu_grouping import (GPUExpertGrouping, GPUGroupingResult, group_tokens_by_expert_auto,
                            group_tokens_by_expert_fast, group_tokens_by_expert_gpu_optimized)
 from .layers import MMFP4Linear

@@ -18,6 +18,7 @@ __all__ = [
     "marlin_gemm_int4", "marlin_gemm_fused_u4", "dequant_fp4", "dequant_int4",
     "dequant_fp4_decode_gemv", "decode_gemv_fp4", "mmfp4_gemm", "dequantize_mmfp4",
     "select_decode_kernel", "fused_gate_up_gemm", "mmfp4_fused_gate_up",
+    "mmfp4_gemm_rowpacked", "rowpacked_gemm_supported",
     "mmfp4_fused_gate_up_marlin", "mmfp4_fused_qkv", "FP4_PER_UINT",
 ]
 
@@ -83,6 +84,34 @@ def marlin_gemm_fp4(A: torch.Tensor, B_packed: torch.Tensor, scales: torch.Tenso
     4083-4098 chooses by M the same way).
     """
     return _gemm("fp4", A, B_packed, scales, None, group_size)
+
+
+def rowpacked_gemm_supported(M: int, N: int, K: int, group_size: int) -> bool:
+    """Shapes the in-place row-packed decode kernel takes (mm_fp4_gemm_rowpacked)."""
+    return (0 < M <= 16 and K % 256 == 0 and group_size > 0 and group_size % 64 == 0
+            and K % group_size == 0 and N % 4 == 0)
+
+
+def mmfp4_gemm_rowpacked(A: torch.Tensor, B_rows: torch.Tensor, scales_rows: torch.Tensor,
+                         group_size: int = 128) -> torch.Tensor:
+    """A [M, K] @ dequant(B_rows)^T with row-packed weights read in place:
+    B_rows [N, K/8] words, scales_rows [N, K/group_size] (the layouts of the
+    reference's MMFP4 kernel, layers/mmfp4_linear.py:549-598), M <= 16."""
+    dev = _lib.require_device(A, B_rows, scales_rows)
+    M, K = A.shape
+    N, K_packed = B_rows.shape
+    if K_packed * FP4_PER_UINT != K:
+        raise ValueError(f"Packed K {K_packed * FP4_PER_UINT} does not match activations K {K}")
+    if tuple(scales_rows.shape) != (N, K // group_size):
+        raise ValueError(f"scales shape {tuple(scales_rows.shape)} != ({N}, {K // group_size})")
+    a = _half(A)
+    b = _packed(B_rows)
+    s = _half(scales_rows)
+    out = torch.empty((M, N), dtype=torch.float16, device=dev)
+    ws = _lib.workspace(dev, int(_lib.load().mm_gemm_workspace_bytes(M, N, K)))
+    _lib.call("mm_fp4_gemm_rowpacked", _lib.ptr(a), _lib.ptr(b), _lib.ptr(s), _lib.ptr(out), M, N,
+              K, group_size, _lib.ptr(ws), ws.numel(), _lib.stream_of(a))
+    return out
 
 
 def marlin_gemm_fp4_tuned(A, B_packed, scales, group_size: int = 32):

@@ -6,9 +6,11 @@ word (n, j) holding inputs 8j..8j+7 of output n (LSB first); scales are
 [n_groups, out_features] or [out_features, n_groups].  The kernels read the
 Marlin layout [in // 8, out]: `MMFP4Linear` converts its weights once (on
 the device, kept as a non-persistent buffer, as the reference keeps its
-`_kernel_packed_weights`), and the functional `mmfp4_gemm` converts per call
-(as the reference's does).  Every M runs the FP4 kernels; the reference's
-M <= 16 path dequantises the whole weight to fp16 and calls F.linear.
+`_kernel_packed_weights`).  The functional `mmfp4_gemm` reads the row-packed
+words in place at decode sizes (M <= 16, K % 256 == 0, group size % 64 == 0:
+mm_fp4_gemm_rowpacked) and converts per call otherwise (as the reference
+does on every call).  Every M runs the FP4 kernels; the reference's M <= 16
+path dequantises the whole weight to fp16 and calls F.linear.
 """
 
 from __future__ import annotations
@@ -50,6 +52,15 @@ def _scales_groups_first(scales: torch.Tensor, out_features: int, n_groups: int)
     return s.to(torch.float16).contiguous()
 
 
+def _scales_rows_first(scales: torch.Tensor, out_features: int, n_groups: int) -> torch.Tensor:
+    """Scales as [out_features, n_groups] (the reference kernel's layout).  A
+    square tensor is read as [n_groups, out_features], as
+    _scales_groups_first reads it, so both paths agree."""
+    if tuple(scales.shape) == (out_features, n_groups) and out_features != n_groups:
+        return scales.to(torch.float16).contiguous()
+    return _scales_groups_first(scales, out_features, n_groups).t().contiguous()
+
+
 def mmfp4_gemm(x: torch.Tensor, packed_weights: torch.Tensor, scales: torch.Tensor,
                group_size: int) -> torch.Tensor:
     """x [M, in] @ dequant(row-packed W [out, in // 8])^T -> [M, out] fp16
@@ -64,7 +75,13 @@ def mmfp4_gemm(x: torch.Tensor, packed_weights: torch.Tensor, scales: torch.Tens
                          f"x.shape[1]={x.shape[1]} vs packed in_features="
                          f"{packed_weights.shape[1] * 8}")
     out_f, in_f = packed_weights.shape[0], packed_weights.shape[1] * 8
-    s = _scales_groups_first(scales, out_f, -(-in_f // group_size))
+    n_groups = -(-in_f // group_size)
+    if kernels.rowpacked_gemm_supported(x.shape[0], out_f, in_f, group_size):
+        # decode sizes: the row-packed words are read in place, no transpose
+        return kernels.mmfp4_gemm_rowpacked(x, _as_words(packed_weights),
+                                            _scales_rows_first(scales, out_f, n_groups),
+                                            group_size)
+    s = _scales_groups_first(scales, out_f, n_groups)
     return kernels.marlin_gemm_fp4(x, rowpacked_to_marlin(packed_weights), s, group_size)
 
 

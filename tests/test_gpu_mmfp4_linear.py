@@ -68,3 +68,40 @@ def test_dispatch_gemm_fp4_and_gemmfp4(rng):
     assert r is out and max_abs_rel(to_np(out), ref) <= TOL
     y = mmfp4.GemmFp4()(to_dev(x[None]), to_dev(p), to_dev(s), g)
     assert tuple(y.shape) == (1, M, N) and max_abs_rel(to_np(y[0]), ref) <= TOL
+
+
+@pytest.mark.parametrize("M,K,N,g", [(1, 4096, 4096, 128), (4, 14336, 4096, 128),
+                                     (16, 4096, 6144, 64), (1, 256, 4, 256), (7, 1024, 100, 128),
+                                     (1, 4096, 28672, 128), (3, 2048, 1028, 64)])
+def test_rowpacked_gemm_in_place(M, K, N, g):
+    """mm_fp4_gemm_rowpacked reads [N, K/8] words and [N, K/g] scales in place
+    (layers/mmfp4_linear.py:549-598 without its per-call transpose): parity
+    with the fp32 reference of the same weights, including the split-K shape
+    14336 -> 4096."""
+    import mmfp4
+    gen = torch.Generator(device="cuda").manual_seed(M * 3 + K + N)
+    w = (torch.randn((N, K), generator=gen, device="cuda") * 0.02).half()
+    a = torch.randn((M, K), generator=gen, device="cuda").half()
+    marlin, scales = mmfp4.quantize_fp4(w, group_size=g)            # [K/8, N], [K/g, N]
+    ref = a.float() @ mmfp4.dequant_fp4(marlin, scales, K, N, g).float()
+    rows, srows = marlin.t().contiguous(), scales.t().contiguous()   # [N, K/8], [N, K/g]
+    announce(f"row-packed gemm M={M} K={K} N={N} g={g}")
+    out = mmfp4.mmfp4_gemm_rowpacked(a, rows, srows, g)
+    assert max_abs_rel(to_np(out), to_np(ref)) <= TOL
+    # the layer-level functional entry takes this path and agrees
+    fn = mmfp4.layers.mmfp4_gemm(a, rows, srows, g)
+    assert torch.equal(fn.view(torch.int16), out.view(torch.int16))
+
+
+def test_rowpacked_gemm_refuses_unsupported_shapes():
+    import mmfp4
+    a = torch.zeros((17, 512), dtype=torch.float16, device="cuda")
+    rows = torch.zeros((64, 64), dtype=torch.int32, device="cuda")
+    s = torch.ones((64, 4), dtype=torch.float16, device="cuda")
+    with pytest.raises(ValueError):                          # M > 16
+        mmfp4.mmfp4_gemm_rowpacked(a, rows, s, 128)
+    with pytest.raises(ValueError):                          # K % 256 != 0
+        mmfp4.mmfp4_gemm_rowpacked(a[:1, :384], rows[:, :48], s[:, :3], 128)
+    with pytest.raises(ValueError):                          # group size % 64 != 0
+        mmfp4.mmfp4_gemm_rowpacked(a[:1], rows, torch.ones((64, 16), dtype=torch.float16,
+                                                            device="cuda"), 32)
