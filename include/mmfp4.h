@@ -104,6 +104,18 @@ int mm_fp4_gate_up(const uint16_t* A, const uint32_t* Bg, const uint16_t* Sg, co
                    const uint16_t* Su, uint16_t* C, int M, int N, int K, int group_size, int act,
                    void* ws, size_t ws_bytes, void* stream);
 
+/* mm_fp4_gate_up for row-packed (MMFP4) gate and up matrices read in place:
+ * Bg, Bu [N, K/8] uint32, scales Sg, Su fp16 [K/g, N]; act as mm_fp4_gate_up.
+ * Decode sizes only: M <= 16, K % 256 == 0, g % 64 == 0, N % 8 == 0.
+ * Workspace: mm_gemm_workspace_bytes(M, 2N, K).  Replaces
+ * metal_marlin/kernels_core.py:4762-4774 (mmfp4_fused_gate_up) ->
+ * MetalKernels.mmfp4_fused_gate_up :4269-4408 on its row-packed inputs,
+ * without a transpose of the weights. */
+int mm_fp4_gate_up_rowpacked(const uint16_t* A, const uint32_t* Bg, const uint16_t* Sg,
+                             const uint32_t* Bu, const uint16_t* Su, uint16_t* C, int M, int N,
+                             int K, int group_size, int act, void* ws, size_t ws_bytes,
+                             void* stream);
+
 /* Up to three FP4 products sharing A and K, one output each:
  * C[p] [M, N[p]] = A . dequant(B[p], S[p]), p < nmat <= 3 (B[p] Marlin
  * [K/8, N[p]], S[p] [K/g, N[p]]).  The tables are host arrays of device

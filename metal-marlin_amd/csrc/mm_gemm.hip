@@ -60,7 +60,9 @@ struct SkMulti {
 // SK_PAIR (NT = 2): tile 0 is columns [n0, n0+64) of (B, S, Z) and tile 1
 // the same columns of (B2, S2, Z2).  Split-K partials are [ksplit][M][PW]
 // fp32 with PW = N, 2N for the pair modes (gate at n, up at N + n), or ntot.
-template <bool INT4, int MT, int NT, int SPW, int NW, int FL, int ACT, bool ROWP = false>
+// ROWP: 0 Marlin-layout weights; row-packed [N, K/8] weights with scales
+// [N, K/g] (1) or [K/g, N] (2).
+template <bool INT4, int MT, int NT, int SPW, int NW, int FL, int ACT, int ROWP = 0>
 __global__ void __launch_bounds__(NW * 64)
 k_skinny(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
          const f16* __restrict__ S, const f16* __restrict__ Z, const uint32_t* __restrict__ B2,
@@ -109,10 +111,10 @@ k_skinny(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
   for (int t = 0; t < NT; ++t)
     tl[t] = ONE ? SkTile{B, S, Z, n0 + t * SK_COLS}
                 : (t == 0 ? SkTile{B, S, Z, n0} : SkTile{B2, S2, Z2, n0});
-  if constexpr (ROWP) {
-    // Row-packed weights ([N, K/8] words, [N, K/g] scales): FP4, one tile.
-    static_assert(!INT4 && NT == 1 && ACT == SK_PLAIN, "row-packed: plain FP4 product");
-    rowp_wave<MT, SPW>(A, lda, M, tl[0], N, K, g, blk_st0 + wave * SPW, nrounds, NW * SPW, acc);
+  if constexpr (ROWP != 0) {
+    static_assert(!INT4 && ACT != SK_MULTI, "row-packed: FP4 product or gate/up pair");
+    rowp_wave<MT, NT, SPW, ROWP == 2>(A, lda, M, tl, N, K, g, blk_st0 + wave * SPW, nrounds,
+                                      NW * SPW, acc);
   } else {
     skinny_wave<INT4, MT, NT, SPW, FL>(A, lda, nullptr, 1, M, tl, N, K, g, blk_st0 + wave * SPW,
                                        nrounds, NW * SPW, acc);
@@ -644,7 +646,7 @@ size_t skinny_ws_bytes(int M, int N, int K) {
 // B2/S2/Z2 the up matrix, both [.., N]; the split and workspace are those of
 // the unfused [K, 2N] product (plan_skinny(M, 2N, K)).
 // SK_MULTI: `mp` describes the matrices (N is then mp->ntot, B..Z2 unused).
-template <bool INT4, int MT, int ACT, bool ROWP = false>
+template <bool INT4, int MT, int ACT, int ROWP = 0>
 int launch_skinny(const f16* A, int lda, const uint32_t* B, const f16* S, const f16* Z,
                   const uint32_t* B2, const f16* S2, const f16* Z2, f16* C, int ldc, int M,
                   int N, int K, int g, void* ws, size_t ws_bytes, hipStream_t st,
@@ -671,7 +673,7 @@ int launch_skinny(const f16* A, int lda, const uint32_t* B, const f16* S, const 
   hipLaunchKernelGGL((k_skinny<INT4, MT, NT, SPW, sk_nw<MT>(), FLV, ACT, ROWP>), grid, dim3(sk_nw<MT>() * 64), 0, \
                      st, A, lda, B, S, Z, B2, S2, Z2, C, ldc, M, N, K, g, p.nrounds, part,       \
                      counters, mp ? *mp : none)
-  if constexpr (ROWP) {
+  if constexpr (ROWP != 0) {
     MM_LAUNCH_SK(0);   // pre-scale: rowp_wave applies each lane's own group scale
   } else {
     switch (fl) {
@@ -1056,9 +1058,39 @@ extern "C" int mm_fp4_gemm_rowpacked(const uint16_t* A, const uint32_t* B, const
                    ((uintptr_t)C & 7) == 0,
                "%s: A and the packed weights must be 16-byte aligned, C 8-byte", who);
   if (M == 0) return 0;
-  return launch_skinny<false, 1, SK_PLAIN, true>((const f16*)A, K, B, (const f16*)S, nullptr,
+  return launch_skinny<false, 1, SK_PLAIN, 1>((const f16*)A, K, B, (const f16*)S, nullptr,
                                                  nullptr, nullptr, nullptr, (f16*)C, N, M, N, K,
                                                  g, ws, ws_bytes, (hipStream_t)stream);
+}
+
+extern "C" int mm_fp4_gate_up_rowpacked(const uint16_t* A, const uint32_t* Bg, const uint16_t* Sg,
+                                        const uint32_t* Bu, const uint16_t* Su, uint16_t* C,
+                                        int M, int N, int K, int g, int act, void* ws,
+                                        size_t ws_bytes, void* stream) {
+  const char* who = "mm_fp4_gate_up_rowpacked";
+  MM_CHECK_ARG(act == 0 || act == 1, "%s: act=%d must be 0 or 1", who, act);
+  MM_CHECK_ARG(M >= 0 && N > 0 && K > 0, "%s: bad shape M=%d N=%d K=%d", who, M, N, K);
+  MM_CHECK_ARG(M <= 16, "%s: M=%d: the row-packed decode kernel takes M <= 16 (larger M: "
+               "transpose to the [K/8, N] layout and call mm_fp4_gate_up)", who, M);
+  MM_CHECK_ARG(K % 256 == 0, "%s: K=%d must be divisible by 256", who, K);
+  MM_CHECK_ARG(g > 0 && g % 64 == 0 && K % g == 0,
+               "%s: group_size=%d must be a multiple of 64 dividing K=%d", who, g, K);
+  MM_CHECK_ARG(N % 8 == 0, "%s: N=%d must be divisible by 8", who, N);
+  MM_CHECK_ARG((size_t)N * (size_t)(K / 8) * 4 < ((size_t)1 << 32),
+               "%s: each packed matrix must be under 4 GiB", who);
+  const uintptr_t a16 = (uintptr_t)A | (uintptr_t)Bg | (uintptr_t)Bu;
+  MM_CHECK_ARG((a16 & 15) == 0 && (((uintptr_t)Sg | (uintptr_t)Su) & 7) == 0 &&
+                   ((uintptr_t)C & 7) == 0,
+               "%s: A and the packed weights must be 16-byte aligned, scales and C 8-byte", who);
+  if (M == 0) return 0;
+  const int ldc = act ? N : 2 * N;
+  if (act)
+    return launch_skinny<false, 1, SK_SWIGLU, 2>((const f16*)A, K, Bg, (const f16*)Sg, nullptr,
+                                                 Bu, (const f16*)Su, nullptr, (f16*)C, ldc, M,
+                                                 N, K, g, ws, ws_bytes, (hipStream_t)stream);
+  return launch_skinny<false, 1, SK_PAIR, 2>((const f16*)A, K, Bg, (const f16*)Sg, nullptr, Bu,
+                                             (const f16*)Su, nullptr, (f16*)C, ldc, M, N, K, g, ws,
+                                             ws_bytes, (hipStream_t)stream);
 }
 
 extern "C" int mm_u4_gemm(const uint16_t* A, const uint32_t* B, const uint16_t* S,

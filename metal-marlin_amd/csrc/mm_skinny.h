@@ -265,9 +265,12 @@ MM_DEV void skinny_wave(const f16* __restrict__ A, int lda, const int* __restric
 // of an MFMA can straddle a group, so weights are scaled before the MFMA
 // (pre-scale, bit-exact fp16 values).  Requires K % 256 == 0 (every round lies
 // inside K) and SPW == 8.
-template <int MT, int SPW>
-MM_DEV void rowp_wave(const f16* __restrict__ A, int lda, int M, const SkTile& tl, int N, int K,
-                      int g, int st0, int nrounds, int ststride, f32x4 (&acc)[MT][1][4]) {
+template <int MT, int NT, int SPW, bool SG>
+MM_DEV void rowp_wave(const f16* __restrict__ A, int lda, int M, const SkTile (&tl)[NT], int N,
+                      int K, int g, int st0, int nrounds, int ststride,
+                      f32x4 (&acc)[MT][NT][4]) {
+  // SG: scales groups-first [K/g, N] (else [N, K/g]).  NT tiles (gate and up
+  // matrices of a pair) share the activations.
   static_assert(SPW == 8, "a lane's run of rows is one 64-k piece of a scale group");
   const int lane = threadIdx.x & 63;
   const int c = lane & 15, q = lane >> 4;
@@ -276,28 +279,40 @@ MM_DEV void rowp_wave(const f16* __restrict__ A, int lda, int M, const SkTile& t
   uint32_t aoff[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) aoff[mt] = (uint32_t)min(mt * 16 + c, M - 1) * (uint32_t)lda * 2u;
-  const uint32_t col = (uint32_t)min(tl.col0 + 4 * c, N - 4);   // lane's first column
+  uint32_t col[NT];                                             // lane's first column per tile
+#pragma unroll
+  for (int t = 0; t < NT; ++t) col[t] = (uint32_t)min(tl[t].col0 + 4 * c, N - 4);
   st0 = __builtin_amdgcn_readfirstlane(st0);
   for (int r = 0; r < nrounds; ++r) {
     const int stb = st0 + r * ststride;
     if (stb >= nsteps) break;
     const uint32_t kp0 = (uint32_t)(4 * stb + q * SPW);        // lane's first word row
     const uint32_t gi = kp0 * 8u / (uint32_t)g;
-    f16 sc[4];
+    f16 sc[NT][4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      sc[j] = sanitize_scale(*at_bytes<f16>(tl.S, ((col + j) * (uint32_t)G + gi) * 2u));
-    u32x4 w[4][SPW / 4];                                        // [column][4 rows]
+    for (int t = 0; t < NT; ++t) {
+      if constexpr (SG) {
+        const f16x4 s4 = *at_bytes<f16x4>(tl[t].S, (gi * (uint32_t)N + col[t]) * 2u);
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < 4; ++j) sc[t][j] = sanitize_scale(s4[j]);
+      } else {
 #pragma unroll
-      for (int u = 0; u < SPW / 4; ++u) {
-        // Plain loads: the two 16-byte pieces of a lane share 128-byte lines
-        // with the neighbouring lanes' pieces, read by the next instruction; a
-        // non-temporal hint made the layer GEMMs ~15% slower (4096x28672 at
-        // M=1 21.5 -> 18.4 us without it).
-        w[j][u] = *at_bytes<u32x4>(tl.B, ((col + j) * (uint32_t)KP + kp0 + 4u * u) * 4u);
+        for (int j = 0; j < 4; ++j)
+          sc[t][j] = sanitize_scale(*at_bytes<f16>(tl[t].S, ((col[t] + j) * (uint32_t)G + gi) * 2u));
       }
+    }
+    u32x4 w[NT][4][SPW / 4];                                    // [tile][column][4 rows]
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int u = 0; u < SPW / 4; ++u)
+          // Plain loads: the two 16-byte pieces of a lane share 128-byte lines
+          // with the neighbouring lanes' pieces, read by the next instruction;
+          // a non-temporal hint made the layer GEMMs ~15% slower (4096x28672
+          // at M=1 21.5 -> 18.4 us without it).
+          w[t][j][u] = *at_bytes<u32x4>(tl[t].B, ((col[t] + j) * (uint32_t)KP + kp0 + 4u * u) * 4u);
     f16x8 a[SPW][MT];
 #pragma unroll
     for (int i = 0; i < SPW; ++i)
@@ -306,12 +321,15 @@ MM_DEV void rowp_wave(const f16* __restrict__ A, int lda, int M, const SkTile& t
 #pragma unroll
     for (int i = 0; i < SPW; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const f16x8 b = WordDq<false>::run(w[j][i >> 2][i & 3], sc[j], (f16)0);
+      for (int t = 0; t < NT; ++t)
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-          acc[mt][0][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i][mt], b, acc[mt][0][j], 0, 0, 0);
-      }
+        for (int j = 0; j < 4; ++j) {
+          const f16x8 b = WordDq<false>::run(w[t][j][i >> 2][i & 3], sc[t][j], (f16)0);
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+            acc[mt][t][j] =
+                __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i][mt], b, acc[mt][t][j], 0, 0, 0);
+        }
   }
 }
 

@@ -48,11 +48,13 @@ def test_gate_up_vs_fp32_reference(M, K, N, g):
     assert torch.equal(pair, mmfp4.fused_gate_up_gemm(x, gp, gs, up, us, g))
 
 
-def test_gate_up_rowpacked_vs_oracle(rng):
+@pytest.mark.parametrize("M,K,N,g", [(3, 512, 256, 128), (1, 4096, 14336, 128),
+                                     (16, 2048, 1024, 64), (40, 512, 256, 128)])
+def test_gate_up_rowpacked_vs_oracle(rng, M, K, N, g):
     """mmfp4_fused_gate_up on row-packed [N, K/8] weights (the reference's
-    documented layout) against the numpy oracle."""
+    documented layout) against the numpy oracle: read in place at decode
+    sizes (M <= 16), transposed per call above."""
     import mmfp4
-    M, K, N, g = 3, 512, 256, 128
     wg = rng.normal(0, 0.02, (N, K)).astype(np.float16)
     wu = rng.normal(0, 0.02, (N, K)).astype(np.float16)
     gp, gs = ofp4.quantize_fp4(wg, g)
@@ -62,7 +64,7 @@ def test_gate_up_rowpacked_vs_oracle(rng):
     hg = xf @ ofp4.dequant_fp4_f32(gp, gs, g)
     hu = xf @ ofp4.dequant_fp4_f32(up, us, g)
     ref = hg / (1.0 + np.exp(-hg)) * hu
-    announce("gate_up row-packed vs oracle")
+    announce(f"gate_up row-packed vs oracle M={M} K={K} N={N} g={g}")
     out = mmfp4.mmfp4_fused_gate_up(to_dev(x), to_dev(np.ascontiguousarray(gp.T)), to_dev(gs),
                                     to_dev(np.ascontiguousarray(up.T)), to_dev(us), g)
     assert max_abs_rel(to_np(out), ref) <= TOL
