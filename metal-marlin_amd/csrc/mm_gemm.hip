@@ -646,6 +646,10 @@ size_t skinny_ws_bytes(int M, int N, int K) {
 // B2/S2/Z2 the up matrix, both [.., N]; the split and workspace are those of
 // the unfused [K, 2N] product (plan_skinny(M, 2N, K)).
 // SK_MULTI: `mp` describes the matrices (N is then mp->ntot, B..Z2 unused).
+#ifndef MM_ROWP_TILES
+#define MM_ROWP_TILES 1      // 64-column tiles per block of the plain row-packed product; 2
+                             // measured slower at M=1 (4096x6144 10.1 -> 18.8 us)
+#endif
 template <bool INT4, int MT, int ACT, int ROWP = 0>
 int launch_skinny(const f16* A, int lda, const uint32_t* B, const f16* S, const f16* Z,
                   const uint32_t* B2, const f16* S2, const f16* Z2, f16* C, int ldc, int M,
@@ -653,8 +657,10 @@ int launch_skinny(const f16* A, int lda, const uint32_t* B, const f16* S, const 
                   const SkMulti* mp = nullptr) {
   const int PW = ACT == SK_PLAIN || ACT == SK_MULTI ? N : 2 * N;
   const SkinnyPlan p = plan_skinny(M, PW, K);
-  constexpr int NT = ACT == SK_PLAIN || ACT == SK_MULTI ? sk_nt<MT>() : 2;
-  const int gx = ACT == SK_PLAIN ? p.ntiles : (ACT == SK_MULTI ? mp->tile0[3] : mm_cdiv(N, SK_COLS));
+  constexpr int NT =
+      ACT == SK_PLAIN || ACT == SK_MULTI ? (ROWP != 0 ? MM_ROWP_TILES : sk_nt<MT>()) : 2;
+  const int gx = ACT == SK_PLAIN ? mm_cdiv(N, NT * SK_COLS)
+                                 : (ACT == SK_MULTI ? mp->tile0[3] : mm_cdiv(N, SK_COLS));
   const SkMulti none{};
   MM_CHECK_ARG(gx <= SK_MAX_TILES, "gemm: N=%d exceeds the supported %d columns", N,
                SK_MAX_TILES * SK_COLS);
