@@ -104,6 +104,17 @@ int mm_fp4_gate_up(const uint16_t* A, const uint32_t* Bg, const uint16_t* Sg, co
                    const uint16_t* Su, uint16_t* C, int M, int N, int K, int group_size, int act,
                    void* ws, size_t ws_bytes, void* stream);
 
+/* C[M,N] = A[M,K] . dequant_fp4(B, scales) with Marlin-layout words B
+ * [K/8, N] and scales in the MMFP4 kernel's [N, K/g] layout, read in place.
+ * Decode sizes only (M <= 16); otherwise as mm_fp4_gemm (K % 8 == 0,
+ * N % 4 == 0, group_size % 8 == 0 dividing K).  Workspace as
+ * mm_gemm_workspace_bytes(M, N, K).  Replaces metal_marlin/kernels_core.py:
+ * 4804-4812 (mmfp4_gemm) -> MetalKernels.mmfp4_gemm :4550-4633, whose
+ * kernel takes the scales [N, n_groups], without transposing them. */
+int mm_fp4_gemm_mmfp4(const uint16_t* A, const uint32_t* B, const uint16_t* scales, uint16_t* C,
+                      int M, int N, int K, int group_size, void* ws, size_t ws_bytes,
+                      void* stream);
+
 /* mm_fp4_gate_up for row-packed (MMFP4) gate and up matrices read in place:
  * Bg, Bu [N, K/8] uint32, scales Sg, Su fp16 [K/g, N]; act as mm_fp4_gate_up.
  * Decode sizes only: M <= 16, K % 256 == 0, g % 64 == 0, N % 8 == 0.

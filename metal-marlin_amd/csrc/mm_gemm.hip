@@ -61,7 +61,7 @@ struct SkMulti {
 // the same columns of (B2, S2, Z2).  Split-K partials are [ksplit][M][PW]
 // fp32 with PW = N, 2N for the pair modes (gate at n, up at N + n), or ntot.
 // ROWP: 0 Marlin-layout weights; row-packed [N, K/8] weights with scales
-// [N, K/g] (1) or [K/g, N] (2).
+// [N, K/g] (1) or [K/g, N] (2); 3 Marlin-layout weights with scales [N, K/g].
 template <bool INT4, int MT, int NT, int SPW, int NW, int FL, int ACT, int ROWP = 0>
 __global__ void __launch_bounds__(NW * 64)
 k_skinny(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
@@ -111,13 +111,14 @@ k_skinny(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
   for (int t = 0; t < NT; ++t)
     tl[t] = ONE ? SkTile{B, S, Z, n0 + t * SK_COLS}
                 : (t == 0 ? SkTile{B, S, Z, n0} : SkTile{B2, S2, Z2, n0});
-  if constexpr (ROWP != 0) {
+  if constexpr (ROWP == 1 || ROWP == 2) {
     static_assert(!INT4 && ACT != SK_MULTI, "row-packed: FP4 product or gate/up pair");
     rowp_wave<MT, NT, SPW, ROWP == 2>(A, lda, M, tl, N, K, g, blk_st0 + wave * SPW, nrounds,
                                       NW * SPW, acc);
   } else {
-    skinny_wave<INT4, MT, NT, SPW, FL>(A, lda, nullptr, 1, M, tl, N, K, g, blk_st0 + wave * SPW,
-                                       nrounds, NW * SPW, acc);
+    skinny_wave<INT4, MT, NT, SPW, FL, false, ROWP == 3>(A, lda, nullptr, 1, M, tl, N, K, g,
+                                                         blk_st0 + wave * SPW, nrounds, NW * SPW,
+                                                         acc);
   }
   skinny_block_reduce<MT, NT, NW>(red, acc, M);
 
@@ -240,7 +241,7 @@ k_skinny(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
 // 8..15 the second slab against columns 8..15, so D[m][c] + D[8+m][8+c] is
 // row m of the product for column group c.  Half-width tiles double the
 // grid of narrow layers without a K split.
-template <bool INT4, int SPW, int NW, int FL>
+template <bool INT4, int SPW, int NW, int FL, bool SROW = false>
 __global__ void __launch_bounds__(NW * 64)
 k_skinny_dual(const f16* __restrict__ A, const uint32_t* __restrict__ B,
               const f16* __restrict__ S, const f16* __restrict__ Z, f16* __restrict__ C, int M,
@@ -253,7 +254,7 @@ k_skinny_dual(const f16* __restrict__ A, const uint32_t* __restrict__ B,
 #pragma unroll
   for (int j = 0; j < 4; ++j) acc[0][0][j] = f32x4{0, 0, 0, 0};
   const SkTile tl[1] = {SkTile{B, S, Z, n0}};
-  skinny_wave<INT4, 1, 1, SPW, FL, true>(A, K, nullptr, 1, M, tl, N, K, g, wave * SPW, nrounds,
+  skinny_wave<INT4, 1, 1, SPW, FL, true, SROW>(A, K, nullptr, 1, M, tl, N, K, g, wave * SPW, nrounds,
                                          NW * SPW, acc);
   // Rows 8..15 (lanes q >= 2) hold the second slab's sums: reduce all 16.
   skinny_block_reduce<1, 1, NW>(red, acc, 16);
@@ -658,7 +659,8 @@ int launch_skinny(const f16* A, int lda, const uint32_t* B, const f16* S, const 
   const int PW = ACT == SK_PLAIN || ACT == SK_MULTI ? N : 2 * N;
   const SkinnyPlan p = plan_skinny(M, PW, K);
   constexpr int NT =
-      ACT == SK_PLAIN || ACT == SK_MULTI ? (ROWP != 0 ? MM_ROWP_TILES : sk_nt<MT>()) : 2;
+      ACT == SK_PLAIN || ACT == SK_MULTI ? (ROWP == 1 || ROWP == 2 ? MM_ROWP_TILES : sk_nt<MT>())
+                                         : 2;
   const int gx = ACT == SK_PLAIN ? mm_cdiv(N, NT * SK_COLS)
                                  : (ACT == SK_MULTI ? mp->tile0[3] : mm_cdiv(N, SK_COLS));
   const SkMulti none{};
@@ -679,7 +681,7 @@ int launch_skinny(const f16* A, int lda, const uint32_t* B, const f16* S, const 
   hipLaunchKernelGGL((k_skinny<INT4, MT, NT, SPW, sk_nw<MT>(), FLV, ACT, ROWP>), grid, dim3(sk_nw<MT>() * 64), 0, \
                      st, A, lda, B, S, Z, B2, S2, Z2, C, ldc, M, N, K, g, p.nrounds, part,       \
                      counters, mp ? *mp : none)
-  if constexpr (ROWP != 0) {
+  if constexpr (ROWP == 1 || ROWP == 2) {
     MM_LAUNCH_SK(0);   // pre-scale: rowp_wave applies each lane's own group scale
   } else {
     switch (fl) {
@@ -731,7 +733,7 @@ bool use_dual(int M, int N, int K, int g) {
          mm_cdiv(N, SK_COLS) < MM_SK_DUAL_BELOW && mm_cdiv(N, 32) >= MM_SK_DUAL_MIN_TILES;
 }
 
-template <bool INT4>
+template <bool INT4, bool SROW = false>
 int launch_dual(const f16* A, const uint32_t* B, const f16* S, const f16* Z, f16* C, int M, int N,
                 int K, int g, hipStream_t st) {
   constexpr int SPW = MM_SK_DUAL_SPW, NW = MM_SK_DUAL_NW;
@@ -739,7 +741,7 @@ int launch_dual(const f16* A, const uint32_t* B, const f16* S, const f16* Z, f16
   const int nrounds = mm_cdiv(nsteps, NW * SPW);
   const int fl = flush_steps(g / 2, SPW);              // 64-k steps per scale group
 #define MM_LAUNCH_DU(FLV)                                                                      \
-  hipLaunchKernelGGL((k_skinny_dual<INT4, SPW, NW, FLV>), dim3(mm_cdiv(N, 32)), dim3(NW * 64), 0, \
+  hipLaunchKernelGGL((k_skinny_dual<INT4, SPW, NW, FLV, SROW>), dim3(mm_cdiv(N, 32)), dim3(NW * 64), 0, \
                      st, A, B, S, Z, C, M, N, K, g, nrounds)
   switch (fl) {
     case 1: MM_LAUNCH_DU(1); break;
@@ -1067,6 +1069,31 @@ extern "C" int mm_fp4_gemm_rowpacked(const uint16_t* A, const uint32_t* B, const
   return launch_skinny<false, 1, SK_PLAIN, 1>((const f16*)A, K, B, (const f16*)S, nullptr,
                                                  nullptr, nullptr, nullptr, (f16*)C, N, M, N, K,
                                                  g, ws, ws_bytes, (hipStream_t)stream);
+}
+
+extern "C" int mm_fp4_gemm_mmfp4(const uint16_t* A, const uint32_t* B, const uint16_t* S,
+                                 uint16_t* C, int M, int N, int K, int g, void* ws,
+                                 size_t ws_bytes, void* stream) {
+  const char* who = "mm_fp4_gemm_mmfp4";
+  MM_CHECK_ARG(M >= 0 && N > 0 && K > 0, "%s: bad shape M=%d N=%d K=%d", who, M, N, K);
+  MM_CHECK_ARG(M <= 16, "%s: M=%d: decode sizes only (M <= 16); larger M: transpose the "
+               "scales to [K/g, N] and call mm_fp4_gemm", who, M);
+  MM_CHECK_ARG(K % 8 == 0, "%s: K=%d must be divisible by 8", who, K);
+  MM_CHECK_ARG(N % 4 == 0, "%s: N=%d must be divisible by 4", who, N);
+  MM_CHECK_ARG(g > 0 && g % 8 == 0 && K % g == 0,
+               "%s: group_size=%d must be a multiple of 8 dividing K=%d", who, g, K);
+  MM_CHECK_ARG((size_t)(K / 8) * (size_t)N * 4 < ((size_t)1 << 32),
+               "%s: the packed weights must be under 4 GiB", who);
+  MM_CHECK_ARG(((uintptr_t)A & 15) == 0 && ((uintptr_t)B & 15) == 0 && ((uintptr_t)S & 1) == 0 &&
+                   ((uintptr_t)C & 7) == 0,
+               "%s: A and the packed weights must be 16-byte aligned, C 8-byte", who);
+  if (M == 0) return 0;
+  if (use_dual(M, N, K, g))
+    return launch_dual<false, true>((const f16*)A, B, (const f16*)S, nullptr, (f16*)C, M, N, K, g,
+                                    (hipStream_t)stream);
+  return launch_skinny<false, 1, SK_PLAIN, 3>((const f16*)A, K, B, (const f16*)S, nullptr,
+                                              nullptr, nullptr, nullptr, (f16*)C, N, M, N, K, g,
+                                              ws, ws_bytes, (hipStream_t)stream);
 }
 
 extern "C" int mm_fp4_gate_up_rowpacked(const uint16_t* A, const uint32_t* Bg, const uint16_t* Sg,

@@ -90,6 +90,20 @@ MM_DEV const T* at_bytes(const void* base, uint32_t off) {
   return (const T*)((const char*)base + off);
 }
 
+// Scales (or zeros) of group gi for columns col .. col+3: [K/g, N] storage
+// (one 8-byte load) or, with SROW, [N, K/g] storage of G = K/g groups per row.
+template <bool SROW>
+MM_DEV f16x4 load_scales4(const f16* S, uint32_t gi, uint32_t col, int N, int G) {
+  if constexpr (!SROW) {
+    return *at_bytes<f16x4>(S, (gi * (uint32_t)N + col) * 2u);
+  } else {
+    f16x4 v;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = *at_bytes<f16>(S, ((col + j) * (uint32_t)G + gi) * 2u);
+    return v;
+  }
+}
+
 // One 64-column tile of a packed weight matrix: its packed words, scales and
 // (INT4) zeros, all [.., N] with row stride N, and the tile's first column.
 // Tiles of one wave may come from different matrices of the same shape.
@@ -106,7 +120,9 @@ struct SkTile {
 // group_size == 32*FL*k for an integer k), or 0 for pre-scale.
 // Rows >= M and columns past N compute values that are never stored: their
 // addresses are clamped into the matrix so no load is predicated.
-template <bool INT4, int MT, int NT, int SPW, int FL, bool DUAL = false>
+// SROW: scales (and zeros) stored [N, K/g] (the reference MMFP4 kernel's
+// layout) instead of [K/g, N]: the four columns' values are four 2-byte loads.
+template <bool INT4, int MT, int NT, int SPW, int FL, bool DUAL = false, bool SROW = false>
 MM_DEV void skinny_wave(const f16* __restrict__ A, int lda, const int* __restrict__ rowmap,
                         int rowdiv, int M, const SkTile (&tl)[NT], int N, int K, int g,
                         int st0, int nrounds, int ststride, f32x4 (&acc)[MT][NT][4]) {
@@ -149,9 +165,8 @@ MM_DEV void skinny_wave(const f16* __restrict__ A, int lda, const int* __restric
         const uint32_t gi = (uint32_t)((stg * 32 * SLAB) / g);      // scalar
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-          s4[f][t] = *at_bytes<f16x4>(tl[t].S, (gi * (uint32_t)N + coff[t]) * 2u);
-          if constexpr (INT4)
-            z4[f][t] = *at_bytes<f16x4>(tl[t].Z, (gi * (uint32_t)N + coff[t]) * 2u);
+          s4[f][t] = load_scales4<SROW>(tl[t].S, gi, coff[t], N, K / g);
+          if constexpr (INT4) z4[f][t] = load_scales4<SROW>(tl[t].Z, gi, coff[t], N, K / g);
         }
       }
     }
@@ -186,9 +201,9 @@ MM_DEV void skinny_wave(const f16* __restrict__ A, int lda, const int* __restric
         const uint32_t gi = (uint32_t)((kp * 8) / g);
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-          const f16x4 s4 = *at_bytes<f16x4>(tl[t].S, (gi * (uint32_t)N + coff[t]) * 2u);
+          const f16x4 s4 = load_scales4<SROW>(tl[t].S, gi, coff[t], N, K / g);
           f16x4 z4 = {0, 0, 0, 0};
-          if constexpr (INT4) z4 = *at_bytes<f16x4>(tl[t].Z, (gi * (uint32_t)N + coff[t]) * 2u);
+          if constexpr (INT4) z4 = load_scales4<SROW>(tl[t].Z, gi, coff[t], N, K / g);
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             f16 nz = 0;

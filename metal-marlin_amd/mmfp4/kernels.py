@@ -337,6 +337,21 @@ def mmfp4_gemm(A: torch.Tensor, B_packed: torch.Tensor, B_scales: torch.Tensor,
     :4550-4633): B_packed [K/8, N], B_scales [N, K/group_size]; A [M, K]."""
     K = B_packed.shape[0] * FP4_PER_UINT
     N = B_packed.shape[1]
+    M = 1
+    for d in A.shape[:-1]:
+        M *= d
+    if (0 < M <= 16 and A.shape[-1] == K and N % 4 == 0 and group_size > 0
+            and group_size % 8 == 0 and K % group_size == 0
+            and tuple(B_scales.shape) == (N, K // group_size)):
+        # decode sizes: the [N, K/g] scales are read in place (mm_fp4_gemm_mmfp4)
+        dev = _lib.require_device(A, B_packed, B_scales)
+        a = _half(A.reshape(M, K))
+        b, s = _packed(B_packed), _half(B_scales)
+        out = torch.empty((M, N), dtype=torch.float16, device=dev)
+        ws = _lib.workspace(dev, int(_lib.load().mm_gemm_workspace_bytes(M, N, K)))
+        _lib.call("mm_fp4_gemm_mmfp4", _lib.ptr(a), _lib.ptr(b), _lib.ptr(s), _lib.ptr(out), M, N,
+                  K, group_size, _lib.ptr(ws), ws.numel(), _lib.stream_of(a))
+        return out.reshape(*A.shape[:-1], N)
     return marlin_gemm_fp4(A, B_packed, _scales_from_mmfp4(B_scales, K, N, group_size),
                            group_size)
 

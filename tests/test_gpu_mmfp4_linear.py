@@ -105,3 +105,27 @@ def test_rowpacked_gemm_refuses_unsupported_shapes():
     with pytest.raises(ValueError):                          # group size % 64 != 0
         mmfp4.mmfp4_gemm_rowpacked(a[:1], rows, torch.ones((64, 16), dtype=torch.float16,
                                                             device="cuda"), 32)
+
+
+@pytest.mark.parametrize("M,K,N,g", [(1, 4096, 4096, 128), (8, 14336, 4096, 128),
+                                     (16, 512, 100, 32), (3, 4096, 6144, 64),
+                                     (40, 512, 256, 128)])
+def test_kernels_mmfp4_gemm_scales_in_place(M, K, N, g):
+    """kernels.mmfp4_gemm (kernels_core.py:4804-4812): Marlin-layout words with
+    the MMFP4 kernel's [N, K/g] scales.  Decode sizes read the scales in place
+    (mm_fp4_gemm_mmfp4); M > 16 transposes them.  Parity with the fp32
+    reference."""
+    import mmfp4
+    gen = torch.Generator(device="cuda").manual_seed(M + 5 * K + N)
+    w = (torch.randn((N, K), generator=gen, device="cuda") * 0.02).half()
+    a = torch.randn((M, K), generator=gen, device="cuda").half()
+    p, s = mmfp4.quantize_fp4(w, group_size=g)
+    ref = a.float() @ mmfp4.dequant_fp4(p, s, K, N, g).float()
+    announce(f"kernels.mmfp4_gemm M={M} K={K} N={N} g={g}")
+    out = mmfp4.mmfp4_gemm(a, p, s.t().contiguous(), g)
+    assert out.shape == (M, N)
+    assert max_abs_rel(to_np(out), to_np(ref)) <= TOL
+    if M <= 8 and K * N <= 4096 * 6144:
+        # The two-slab decode kernel serves both scale layouts with the same
+        # summation order: the results must agree bit for bit.
+        assert torch.equal(out, mmfp4.marlin_gemm_fp4(a, p, s, g))
