@@ -241,7 +241,9 @@ k_skinny(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
 // 8..15 the second slab against columns 8..15, so D[m][c] + D[8+m][8+c] is
 // row m of the product for column group c.  Half-width tiles double the
 // grid of narrow layers without a K split.
-template <bool INT4, int SPW, int NW, int FL, bool SROW = false>
+// ROWP: row-packed FP4 words [N, K/8] with [N, K/g] scales (rowp_wave; SPW == 8,
+// K % 512 == 0).
+template <bool INT4, int SPW, int NW, int FL, bool SROW = false, bool ROWP = false>
 __global__ void __launch_bounds__(NW * 64)
 k_skinny_dual(const f16* __restrict__ A, const uint32_t* __restrict__ B,
               const f16* __restrict__ S, const f16* __restrict__ Z, f16* __restrict__ C, int M,
@@ -254,8 +256,11 @@ k_skinny_dual(const f16* __restrict__ A, const uint32_t* __restrict__ B,
 #pragma unroll
   for (int j = 0; j < 4; ++j) acc[0][0][j] = f32x4{0, 0, 0, 0};
   const SkTile tl[1] = {SkTile{B, S, Z, n0}};
-  skinny_wave<INT4, 1, 1, SPW, FL, true, SROW>(A, K, nullptr, 1, M, tl, N, K, g, wave * SPW, nrounds,
-                                         NW * SPW, acc);
+  if constexpr (ROWP)
+    rowp_wave<1, 1, SPW, false, true>(A, K, M, tl, N, K, g, wave * SPW, nrounds, NW * SPW, acc);
+  else
+    skinny_wave<INT4, 1, 1, SPW, FL, true, SROW>(A, K, nullptr, 1, M, tl, N, K, g, wave * SPW,
+                                                 nrounds, NW * SPW, acc);
   // Rows 8..15 (lanes q >= 2) hold the second slab's sums: reduce all 16.
   skinny_block_reduce<1, 1, NW>(red, acc, 16);
   if (wave != 0) return;
@@ -755,6 +760,10 @@ int launch_dual(const f16* A, const uint32_t* B, const f16* S, const f16* Z, f16
   return 0;
 }
 
+#ifndef MM_ROWP_DUAL
+#define MM_ROWP_DUAL 1
+#endif
+
 #ifndef MM_ST_NW
 #define MM_ST_NW 8
 #endif
@@ -1066,6 +1075,16 @@ extern "C" int mm_fp4_gemm_rowpacked(const uint16_t* A, const uint32_t* B, const
                    ((uintptr_t)C & 7) == 0,
                "%s: A and the packed weights must be 16-byte aligned, C 8-byte", who);
   if (M == 0) return 0;
+  if (MM_ROWP_DUAL && K % 512 == 0 && use_dual(M, N, K, g)) {
+    // Two-slab kernel, 32-column blocks over the whole K (the shapes the
+    // Marlin-layout path also gives it).
+    constexpr int NW = 8;
+    hipLaunchKernelGGL((k_skinny_dual<false, 8, NW, 0, false, true>), dim3(mm_cdiv(N, 32)),
+                       dim3(NW * 64), 0, (hipStream_t)stream, (const f16*)A, B, (const f16*)S,
+                       nullptr, (f16*)C, M, N, K, g, mm_cdiv(K / 64, NW * 8));
+    MM_CHECK_LAUNCH("gemm(rowpacked dual)");
+    return 0;
+  }
   return launch_skinny<false, 1, SK_PLAIN, 1>((const f16*)A, K, B, (const f16*)S, nullptr,
                                                  nullptr, nullptr, nullptr, (f16*)C, N, M, N, K,
                                                  g, ws, ws_bytes, (hipStream_t)stream);

@@ -280,7 +280,10 @@ MM_DEV void skinny_wave(const f16* __restrict__ A, int lda, const int* __restric
 // of an MFMA can straddle a group, so weights are scaled before the MFMA
 // (pre-scale, bit-exact fp16 values).  Requires K % 256 == 0 (every round lies
 // inside K) and SPW == 8.
-template <int MT, int NT, int SPW, bool SG>
+// DUAL (M <= 8, K % 512 == 0): a step is 64 k and a round 64 word rows; lanes
+// c < 8 take the round's first 32 rows and lanes c >= 8 the next 32, for the
+// 32 columns of lane group c & 7 (the two-slab scheme of skinny_wave).
+template <int MT, int NT, int SPW, bool SG, bool DUAL = false>
 MM_DEV void rowp_wave(const f16* __restrict__ A, int lda, int M, const SkTile (&tl)[NT], int N,
                       int K, int g, int st0, int nrounds, int ststride,
                       f32x4 (&acc)[MT][NT][4]) {
@@ -289,19 +292,21 @@ MM_DEV void rowp_wave(const f16* __restrict__ A, int lda, int M, const SkTile (&
   static_assert(SPW == 8, "a lane's run of rows is one 64-k piece of a scale group");
   const int lane = threadIdx.x & 63;
   const int c = lane & 15, q = lane >> 4;
+  const int cl = DUAL ? (c & 7) : c, hs = DUAL ? (c >> 3) : 0;
   const int KP = K >> 3, G = K / g;
-  const int nsteps = KP >> 2;                 // K % 256 == 0: whole steps and rounds
+  const int nsteps = DUAL ? KP >> 3 : KP >> 2;   // whole steps and rounds (K % 256, K % 512)
   uint32_t aoff[MT];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) aoff[mt] = (uint32_t)min(mt * 16 + c, M - 1) * (uint32_t)lda * 2u;
+  for (int mt = 0; mt < MT; ++mt) aoff[mt] = (uint32_t)min(mt * 16 + cl, M - 1) * (uint32_t)lda * 2u;
   uint32_t col[NT];                                             // lane's first column per tile
 #pragma unroll
-  for (int t = 0; t < NT; ++t) col[t] = (uint32_t)min(tl[t].col0 + 4 * c, N - 4);
+  for (int t = 0; t < NT; ++t) col[t] = (uint32_t)min(tl[t].col0 + 4 * cl, N - 4);
   st0 = __builtin_amdgcn_readfirstlane(st0);
   for (int r = 0; r < nrounds; ++r) {
     const int stb = st0 + r * ststride;
     if (stb >= nsteps) break;
-    const uint32_t kp0 = (uint32_t)(4 * stb + q * SPW);        // lane's first word row
+    const uint32_t kp0 = DUAL ? (uint32_t)(8 * stb + 32 * hs + q * SPW)   // lane's first word row
+                              : (uint32_t)(4 * stb + q * SPW);
     const uint32_t gi = kp0 * 8u / (uint32_t)g;
     f16 sc[NT][4];
 #pragma unroll

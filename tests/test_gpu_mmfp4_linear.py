@@ -72,7 +72,8 @@ def test_dispatch_gemm_fp4_and_gemmfp4(rng):
 
 @pytest.mark.parametrize("M,K,N,g", [(1, 4096, 4096, 128), (4, 14336, 4096, 128),
                                      (16, 4096, 6144, 64), (1, 256, 4, 256), (7, 1024, 100, 128),
-                                     (1, 4096, 28672, 128), (3, 2048, 1028, 64)])
+                                     (1, 4096, 28672, 128), (3, 2048, 1028, 64),
+                                     (2, 4096, 6144, 128), (8, 1024, 3072, 64), (5, 4608, 4100, 128)])
 def test_rowpacked_gemm_in_place(M, K, N, g):
     """mm_fp4_gemm_rowpacked reads [N, K/8] words and [N, K/g] scales in place
     (layers/mmfp4_linear.py:549-598 without its per-call transpose): parity
