@@ -760,6 +760,9 @@ int launch_dual(const f16* A, const uint32_t* B, const f16* S, const f16* Z, f16
   return 0;
 }
 
+// Row-packed two-slab kernel: 0 never, 1 on the shapes use_dual picks, 2 for
+// every M <= 8 (measured slower outside use_dual's shapes at M=1:
+// 4096x28672 18.7 -> 20.9 us, 14336x4096 12.4 -> 16.7 us).
 #ifndef MM_ROWP_DUAL
 #define MM_ROWP_DUAL 1
 #endif
@@ -1075,7 +1078,7 @@ extern "C" int mm_fp4_gemm_rowpacked(const uint16_t* A, const uint32_t* B, const
                    ((uintptr_t)C & 7) == 0,
                "%s: A and the packed weights must be 16-byte aligned, C 8-byte", who);
   if (M == 0) return 0;
-  if (MM_ROWP_DUAL && K % 512 == 0 && use_dual(M, N, K, g)) {
+  if (MM_ROWP_DUAL && K % 512 == 0 && M <= 8 && (MM_ROWP_DUAL == 2 || use_dual(M, N, K, g))) {
     // Two-slab kernel, 32-column blocks over the whole K (the shapes the
     // Marlin-layout path also gives it).
     constexpr int NW = 8;
