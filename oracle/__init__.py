@@ -19,15 +19,19 @@ Pinning status (what checks each function against something other than itself):
 * `quantize_fp4`                 -- pinned: golden vectors written by importing
   the reference's quantize_fp4.py (tests/golden/make_quantize_fp4_vectors.py),
   plus the nearest-value invariant on random and crafted midpoint inputs.
-* `pack_u4_weights`              -- partially pinned: round-trip bound
-  |w - (q-z)s| <= s/2 inside the clip range, exact min/max mapping, and the
-  reference test-file quantizer on zero-clip-free inputs.  The reference
-  function itself requires Apple MPS and cannot be imported here, so its
-  half-to-even tie behaviour on exact .5 inputs is "parity unpinned".
+* `pack_u4_weights`              -- pinned (tests/test_oracle_pin.py): a
+  float64 nearest-integer brute force of q away from ties, crafted groups
+  where the float32 scale and its fp16 rounding give different q, exact .5
+  ties of w/s + z and of -min/s (half-to-even), and one-signed groups whose
+  zero point lies outside [0, 15] and is stored unclipped; also the round-trip
+  bound and the reference test-file quantizer on clip-free inputs.
 * `gemm_fp4_ref`, `gemm_u4_ref`  -- fp32 dequant+matmul; pinned by the
   zero / linearity / all-ones-large-K closed forms of tests/test_gemm.py and a
   brute-force float64 triple loop on tiny shapes.
 * MoE (`group_tokens_by_expert`, `gather`, `combine`, `moe_mlp_ref`) --
   pinned by the known-answer cases of tests/test_moe.py and a brute-force
   per-token loop on tiny inputs.
+* `router_topk`                  -- pinned (tests/test_oracle_pin.py): a
+  float64 per-row softmax with an explicit descending selection, ties to the
+  lower expert id, ids compared exactly, on random and crafted tied logits.
 """
