@@ -74,14 +74,16 @@ int mm_fp4_gemm(const uint16_t* A, const uint32_t* B, const uint16_t* scales, ui
 
 /* C[M,N] = A[M,K] . dequant_fp4(B, scales)^T for row-packed (MMFP4) weights:
  * B [N, K/8] uint32 (word (n, kp) holds k = 8kp .. 8kp+7 of row n), scales
- * fp16 [N, K/g].  Decode sizes only: M <= 16, K % 256 == 0, g % 64 == 0,
- * N % 4 == 0; the weights are read in place (no transpose).  Workspace as
- * mm_gemm_workspace_bytes(M, N, K).  Replaces metal_marlin/layers/
- * mmfp4_linear.py:549-598 (mmfp4_gemm), which transposes the row-packed
- * words to the [K/8, N] layout on every call (:414-478). */
+ * fp16 [K/g, N] (scales_layout = 0, the layer's canonical [n_groups, N]) or
+ * [N, K/g] (scales_layout = 1, the transposed layout the layer also accepts,
+ * metal_marlin/layers/mmfp4_linear.py:53-86).  Decode sizes only: M <= 16,
+ * K % 256 == 0, g % 64 == 0, N % 4 == 0; weights and scales are read in place
+ * (no transpose).  Workspace as mm_gemm_workspace_bytes(M, N, K).  Replaces
+ * metal_marlin/layers/mmfp4_linear.py:549-598 (mmfp4_gemm), which transposes
+ * the row-packed words to the [K/8, N] layout on every call (:414-478). */
 int mm_fp4_gemm_rowpacked(const uint16_t* A, const uint32_t* B, const uint16_t* scales,
-                          uint16_t* C, int M, int N, int K, int group_size, void* ws,
-                          size_t ws_bytes, void* stream);
+                          uint16_t* C, int M, int N, int K, int group_size, int scales_layout,
+                          void* ws, size_t ws_bytes, void* stream);
 
 /* INT4 asymmetric counterpart.  Replaces metal_marlin/kernels_core.py:1959-2066
  * (marlin_gemm_int4) and metal_marlin/metal_dispatch.py:1863-1937
@@ -105,12 +107,15 @@ int mm_fp4_gate_up(const uint16_t* A, const uint32_t* Bg, const uint16_t* Sg, co
                    void* ws, size_t ws_bytes, void* stream);
 
 /* C[M,N] = A[M,K] . dequant_fp4(B, scales) with Marlin-layout words B
- * [K/8, N] and scales in the MMFP4 kernel's [N, K/g] layout, read in place.
+ * [K/8, N] and scales in the transposed [N, K/g] layout, read in place.
  * Decode sizes only (M <= 16); otherwise as mm_fp4_gemm (K % 8 == 0,
  * N % 4 == 0, group_size % 8 == 0 dividing K).  Workspace as
- * mm_gemm_workspace_bytes(M, N, K).  Replaces metal_marlin/kernels_core.py:
- * 4804-4812 (mmfp4_gemm) -> MetalKernels.mmfp4_gemm :4550-4633, whose
- * kernel takes the scales [N, n_groups], without transposing them. */
+ * mm_gemm_workspace_bytes(M, N, K).  The reference's MMFP4 GEMM
+ * (metal_marlin/kernels_core.py:4804-4812 -> MetalKernels.mmfp4_gemm
+ * :4550-4633, shaders/mmfp4_gemm.metal:570-588) reads [K/g, N] scales, which
+ * mm_fp4_gemm takes; its layer normalises [N, K/g] scales to that layout by a
+ * transpose (layers/mmfp4_linear.py:53-86).  This entry point serves callers
+ * holding [N, K/g] scales without that transpose. */
 int mm_fp4_gemm_mmfp4(const uint16_t* A, const uint32_t* B, const uint16_t* scales, uint16_t* C,
                       int M, int N, int K, int group_size, void* ws, size_t ws_bytes,
                       void* stream);

@@ -241,8 +241,8 @@ k_skinny(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
 // 8..15 the second slab against columns 8..15, so D[m][c] + D[8+m][8+c] is
 // row m of the product for column group c.  Half-width tiles double the
 // grid of narrow layers without a K split.
-// ROWP: row-packed FP4 words [N, K/8] with [N, K/g] scales (rowp_wave; SPW == 8,
-// K % 512 == 0).
+// ROWP: row-packed FP4 words [N, K/8] (rowp_wave; SPW == 8, K % 512 == 0),
+// scales [N, K/g] when SROW, else [K/g, N].
 template <bool INT4, int SPW, int NW, int FL, bool SROW = false, bool ROWP = false>
 __global__ void __launch_bounds__(NW * 64)
 k_skinny_dual(const f16* __restrict__ A, const uint32_t* __restrict__ B,
@@ -257,7 +257,7 @@ k_skinny_dual(const f16* __restrict__ A, const uint32_t* __restrict__ B,
   for (int j = 0; j < 4; ++j) acc[0][0][j] = f32x4{0, 0, 0, 0};
   const SkTile tl[1] = {SkTile{B, S, Z, n0}};
   if constexpr (ROWP)
-    rowp_wave<1, 1, SPW, false, true>(A, K, M, tl, N, K, g, wave * SPW, nrounds, NW * SPW, acc);
+    rowp_wave<1, 1, SPW, !SROW, true>(A, K, M, tl, N, K, g, wave * SPW, nrounds, NW * SPW, acc);
   else
     skinny_wave<INT4, 1, 1, SPW, FL, true, SROW>(A, K, nullptr, 1, M, tl, N, K, g, wave * SPW,
                                                  nrounds, NW * SPW, acc);
@@ -1062,9 +1062,11 @@ extern "C" int mm_fp4_gemm(const uint16_t* A, const uint32_t* B, const uint16_t*
 }
 
 extern "C" int mm_fp4_gemm_rowpacked(const uint16_t* A, const uint32_t* B, const uint16_t* S,
-                                     uint16_t* C, int M, int N, int K, int g, void* ws,
-                                     size_t ws_bytes, void* stream) {
+                                     uint16_t* C, int M, int N, int K, int g, int scales_layout,
+                                     void* ws, size_t ws_bytes, void* stream) {
   const char* who = "mm_fp4_gemm_rowpacked";
+  MM_CHECK_ARG(scales_layout == 0 || scales_layout == 1,
+               "%s: scales_layout=%d must be 0 ([K/g, N]) or 1 ([N, K/g])", who, scales_layout);
   MM_CHECK_ARG(M >= 0 && N > 0 && K > 0, "%s: bad shape M=%d N=%d K=%d", who, M, N, K);
   MM_CHECK_ARG(M <= 16, "%s: M=%d: the row-packed decode kernel takes M <= 16 (larger M: "
                "transpose to the [K/8, N] layout and call mm_fp4_gemm)", who, M);
@@ -1074,23 +1076,37 @@ extern "C" int mm_fp4_gemm_rowpacked(const uint16_t* A, const uint32_t* B, const
   MM_CHECK_ARG(N % 4 == 0, "%s: N=%d must be divisible by 4", who, N);
   MM_CHECK_ARG((size_t)N * (size_t)(K / 8) * 4 < ((size_t)1 << 32),
                "%s: the packed weights must be under 4 GiB", who);
-  MM_CHECK_ARG(((uintptr_t)A & 15) == 0 && ((uintptr_t)B & 15) == 0 && ((uintptr_t)S & 1) == 0 &&
-                   ((uintptr_t)C & 7) == 0,
-               "%s: A and the packed weights must be 16-byte aligned, C 8-byte", who);
+  // [K/g, N] scales are read as 4 adjacent columns (8 bytes) per lane.
+  const uintptr_t salign = scales_layout == 0 ? 7 : 1;
+  MM_CHECK_ARG(((uintptr_t)A & 15) == 0 && ((uintptr_t)B & 15) == 0 &&
+                   ((uintptr_t)S & salign) == 0 && ((uintptr_t)C & 7) == 0,
+               "%s: A and the packed weights must be 16-byte aligned, C 8-byte (and [K/g, N] "
+               "scales 8-byte)", who);
   if (M == 0) return 0;
+  hipStream_t st = (hipStream_t)stream;
   if (MM_ROWP_DUAL && K % 512 == 0 && M <= 8 && (MM_ROWP_DUAL == 2 || use_dual(M, N, K, g))) {
     // Two-slab kernel, 32-column blocks over the whole K (the shapes the
     // Marlin-layout path also gives it).
     constexpr int NW = 8;
-    hipLaunchKernelGGL((k_skinny_dual<false, 8, NW, 0, false, true>), dim3(mm_cdiv(N, 32)),
-                       dim3(NW * 64), 0, (hipStream_t)stream, (const f16*)A, B, (const f16*)S,
-                       nullptr, (f16*)C, M, N, K, g, mm_cdiv(K / 64, NW * 8));
+    const int nr = mm_cdiv(K / 64, NW * 8);
+    if (scales_layout == 1)
+      hipLaunchKernelGGL((k_skinny_dual<false, 8, NW, 0, true, true>), dim3(mm_cdiv(N, 32)),
+                         dim3(NW * 64), 0, st, (const f16*)A, B, (const f16*)S, nullptr, (f16*)C,
+                         M, N, K, g, nr);
+    else
+      hipLaunchKernelGGL((k_skinny_dual<false, 8, NW, 0, false, true>), dim3(mm_cdiv(N, 32)),
+                         dim3(NW * 64), 0, st, (const f16*)A, B, (const f16*)S, nullptr, (f16*)C,
+                         M, N, K, g, nr);
     MM_CHECK_LAUNCH("gemm(rowpacked dual)");
     return 0;
   }
-  return launch_skinny<false, 1, SK_PLAIN, 1>((const f16*)A, K, B, (const f16*)S, nullptr,
-                                                 nullptr, nullptr, nullptr, (f16*)C, N, M, N, K,
-                                                 g, ws, ws_bytes, (hipStream_t)stream);
+  if (scales_layout == 1)
+    return launch_skinny<false, 1, SK_PLAIN, 1>((const f16*)A, K, B, (const f16*)S, nullptr,
+                                                nullptr, nullptr, nullptr, (f16*)C, N, M, N, K,
+                                                g, ws, ws_bytes, st);
+  return launch_skinny<false, 1, SK_PLAIN, 2>((const f16*)A, K, B, (const f16*)S, nullptr,
+                                              nullptr, nullptr, nullptr, (f16*)C, N, M, N, K, g,
+                                              ws, ws_bytes, st);
 }
 
 extern "C" int mm_fp4_gemm_mmfp4(const uint16_t* A, const uint32_t* B, const uint16_t* S,

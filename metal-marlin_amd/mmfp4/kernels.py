@@ -92,25 +92,38 @@ def rowpacked_gemm_supported(M: int, N: int, K: int, group_size: int) -> bool:
             and K % group_size == 0 and N % 4 == 0)
 
 
-def mmfp4_gemm_rowpacked(A: torch.Tensor, B_rows: torch.Tensor, scales_rows: torch.Tensor,
+def _scales_layout(scales: torch.Tensor, N: int, n_groups: int, name: str = "scales") -> int:
+    """0 for [n_groups, N] (the reference's canonical layout, read first when
+    the tensor is square), 1 for [N, n_groups]; the same shape test as
+    layers/mmfp4_linear.py:53-86 (_optimized_scale_load)."""
+    shape = tuple(scales.shape)
+    if shape == (n_groups, N):
+        return 0
+    if shape == (N, n_groups):
+        return 1
+    raise ValueError(f"{name} shape {shape} is neither ({n_groups}, {N}) nor ({N}, {n_groups})")
+
+
+def mmfp4_gemm_rowpacked(A: torch.Tensor, B_rows: torch.Tensor, scales: torch.Tensor,
                          group_size: int = 128) -> torch.Tensor:
     """A [M, K] @ dequant(B_rows)^T with row-packed weights read in place:
-    B_rows [N, K/8] words, scales_rows [N, K/group_size] (the layouts of the
-    reference's MMFP4 kernel, layers/mmfp4_linear.py:549-598), M <= 16."""
-    dev = _lib.require_device(A, B_rows, scales_rows)
+    B_rows [N, K/8] words, scales [K/group_size, N] (the layer's canonical
+    layout) or [N, K/group_size] (layers/mmfp4_linear.py:549-598), M <= 16."""
+    dev = _lib.require_device(A, B_rows, scales)
     M, K = A.shape
     N, K_packed = B_rows.shape
     if K_packed * FP4_PER_UINT != K:
         raise ValueError(f"Packed K {K_packed * FP4_PER_UINT} does not match activations K {K}")
-    if tuple(scales_rows.shape) != (N, K // group_size):
-        raise ValueError(f"scales shape {tuple(scales_rows.shape)} != ({N}, {K // group_size})")
+    if group_size <= 0 or K % group_size != 0:
+        raise ValueError(f"K={K} must be divisible by group_size={group_size}")
+    layout = _scales_layout(scales, N, K // group_size)
     a = _half(A)
     b = _packed(B_rows)
-    s = _half(scales_rows)
+    s = _half(scales)
     out = torch.empty((M, N), dtype=torch.float16, device=dev)
     ws = _lib.workspace(dev, int(_lib.load().mm_gemm_workspace_bytes(M, N, K)))
     _lib.call("mm_fp4_gemm_rowpacked", _lib.ptr(a), _lib.ptr(b), _lib.ptr(s), _lib.ptr(out), M, N,
-              K, group_size, _lib.ptr(ws), ws.numel(), _lib.stream_of(a))
+              K, group_size, layout, _lib.ptr(ws), ws.numel(), _lib.stream_of(a))
     return out
 
 
@@ -323,26 +336,26 @@ def decode_gemv_fp4(A: torch.Tensor, B_packed: torch.Tensor, B_scales: torch.Ten
     return out.reshape(-1) if squeeze else out
 
 
-def _scales_from_mmfp4(B_scales: torch.Tensor, K: int, N: int, group_size: int) -> torch.Tensor:
-    # The MMFP4 kernels take scales as [N, K/group_size]
-    # (metal_marlin/shaders/mmfp4_gemm.metal:150-151).
-    if tuple(B_scales.shape) != (N, K // group_size):
-        raise ValueError(f"B_scales shape {tuple(B_scales.shape)} != ({N}, {K // group_size})")
-    return B_scales.t().contiguous()
-
-
 def mmfp4_gemm(A: torch.Tensor, B_packed: torch.Tensor, B_scales: torch.Tensor,
                group_size: int = 128) -> torch.Tensor:
     """MMFP4 fused GEMM (kernels_core.py:4804-4812 -> MetalKernels.mmfp4_gemm
-    :4550-4633): B_packed [K/8, N], B_scales [N, K/group_size]; A [M, K]."""
+    :4550-4633): A [M, K], B_packed [K/8, N], B_scales [K/group_size, N] as the
+    kernel reads them (shaders/mmfp4_gemm.metal:570-588, and the M=1
+    decode_gemv_fp4_wide, decode_gemv.metal:4,40).  Scales given as
+    [N, K/group_size] are accepted when the shape says so unambiguously (the
+    layer's _optimized_scale_load, layers/mmfp4_linear.py:53-86, transposes
+    them); at decode sizes they are read in place (mm_fp4_gemm_mmfp4), else
+    transposed.  A square tensor is read as [K/group_size, N]."""
     K = B_packed.shape[0] * FP4_PER_UINT
     N = B_packed.shape[1]
+    if group_size <= 0 or K % group_size != 0:
+        raise ValueError(f"K={K} must be divisible by group_size={group_size}")
+    if _scales_layout(B_scales, N, K // group_size, "B_scales") == 0:
+        return marlin_gemm_fp4(A, B_packed, B_scales, group_size)
     M = 1
     for d in A.shape[:-1]:
         M *= d
-    if (0 < M <= 16 and A.shape[-1] == K and N % 4 == 0 and group_size > 0
-            and group_size % 8 == 0 and K % group_size == 0
-            and tuple(B_scales.shape) == (N, K // group_size)):
+    if 0 < M <= 16 and A.shape[-1] == K and N % 4 == 0 and group_size % 8 == 0:
         # decode sizes: the [N, K/g] scales are read in place (mm_fp4_gemm_mmfp4)
         dev = _lib.require_device(A, B_packed, B_scales)
         a = _half(A.reshape(M, K))
@@ -352,16 +365,22 @@ def mmfp4_gemm(A: torch.Tensor, B_packed: torch.Tensor, B_scales: torch.Tensor,
         _lib.call("mm_fp4_gemm_mmfp4", _lib.ptr(a), _lib.ptr(b), _lib.ptr(s), _lib.ptr(out), M, N,
                   K, group_size, _lib.ptr(ws), ws.numel(), _lib.stream_of(a))
         return out.reshape(*A.shape[:-1], N)
-    return marlin_gemm_fp4(A, B_packed, _scales_from_mmfp4(B_scales, K, N, group_size),
-                           group_size)
+    return marlin_gemm_fp4(A, B_packed, B_scales.t().contiguous(), group_size)
 
 
 def dequantize_mmfp4(packed: torch.Tensor, scales: torch.Tensor,
                      group_size: int = 128) -> torch.Tensor:
-    """MMFP4 bulk dequant (kernels_core.py:4795-4802) -> [K, N] fp16."""
+    """MMFP4 bulk dequant (kernels_core.py:4795-4802, 4699-4738) -> [K, N]
+    fp16; scales [K/group_size, N] as shaders/mmfp4_dequant.metal reads them
+    (scales[group_idx * N + n]); an unambiguous [N, K/group_size] tensor is
+    transposed."""
     K = packed.shape[0] * FP4_PER_UINT
     N = packed.shape[1]
-    return dequant_fp4(packed, _scales_from_mmfp4(scales, K, N, group_size), K, N, group_size)
+    if group_size <= 0 or K % group_size != 0:
+        raise ValueError(f"K={K} must be divisible by group_size={group_size}")
+    if _scales_layout(scales, N, K // group_size) == 1:
+        scales = scales.t()
+    return dequant_fp4(packed, scales, K, N, group_size)
 
 
 def select_decode_kernel(M: int, N: int, K: int) -> str:

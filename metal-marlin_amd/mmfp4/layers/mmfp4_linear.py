@@ -3,14 +3,16 @@ mmfp4_linear.py:414-478, 549-598, 600-960).
 
 Row-packed means `packed_weights` uint32 [out_features, in_features // 8],
 word (n, j) holding inputs 8j..8j+7 of output n (LSB first); scales are
-[n_groups, out_features] or [out_features, n_groups].  The kernels read the
-Marlin layout [in // 8, out]: `MMFP4Linear` converts its weights once (on
-the device, kept as a non-persistent buffer, as the reference keeps its
-`_kernel_packed_weights`).  The functional `mmfp4_gemm` reads the row-packed
-words in place at decode sizes (M <= 16, K % 256 == 0, group size % 64 == 0:
-mm_fp4_gemm_rowpacked) and converts per call otherwise (as the reference
-does on every call).  Every M runs the FP4 kernels; the reference's M <= 16
-path dequantises the whole weight to fp16 and calls F.linear.
+[n_groups, out_features] or [out_features, n_groups].  At decode sizes
+(M <= 16, K % 256 == 0, group size % 64 == 0) both the functional
+`mmfp4_gemm` and `MMFP4Linear` read the row-packed words and the scales in
+place (mm_fp4_gemm_rowpacked).  Larger M runs the prefill kernels, which read
+the Marlin layout [in // 8, out]: the functional form converts per call (as
+the reference does on every call); the layer converts once on the device and
+keeps the copy as a non-persistent buffer (the reference's
+`_kernel_packed_weights`), rebuilt whenever `packed_weights` is written or
+replaced.  The reference's M <= 16 path dequantises the whole weight to fp16
+and calls F.linear.
 """
 
 from __future__ import annotations
@@ -52,15 +54,6 @@ def _scales_groups_first(scales: torch.Tensor, out_features: int, n_groups: int)
     return s.to(torch.float16).contiguous()
 
 
-def _scales_rows_first(scales: torch.Tensor, out_features: int, n_groups: int) -> torch.Tensor:
-    """Scales as [out_features, n_groups] (the reference kernel's layout).  A
-    square tensor is read as [n_groups, out_features], as
-    _scales_groups_first reads it, so both paths agree."""
-    if tuple(scales.shape) == (out_features, n_groups) and out_features != n_groups:
-        return scales.to(torch.float16).contiguous()
-    return _scales_groups_first(scales, out_features, n_groups).t().contiguous()
-
-
 def mmfp4_gemm(x: torch.Tensor, packed_weights: torch.Tensor, scales: torch.Tensor,
                group_size: int) -> torch.Tensor:
     """x [M, in] @ dequant(row-packed W [out, in // 8])^T -> [M, out] fp16
@@ -78,9 +71,7 @@ def mmfp4_gemm(x: torch.Tensor, packed_weights: torch.Tensor, scales: torch.Tens
     n_groups = -(-in_f // group_size)
     if kernels.rowpacked_gemm_supported(x.shape[0], out_f, in_f, group_size):
         # decode sizes: the row-packed words are read in place, no transpose
-        return kernels.mmfp4_gemm_rowpacked(x, _as_words(packed_weights),
-                                            _scales_rows_first(scales, out_f, n_groups),
-                                            group_size)
+        return kernels.mmfp4_gemm_rowpacked(x, _as_words(packed_weights), scales, group_size)
     s = _scales_groups_first(scales, out_f, n_groups)
     return kernels.marlin_gemm_fp4(x, rowpacked_to_marlin(packed_weights), s, group_size)
 
@@ -121,10 +112,16 @@ class MMFP4Linear(nn.Module):
         self.activation = activation
 
     def _kernel_weights(self, device: torch.device) -> torch.Tensor:
+        # The Marlin-layout copy is keyed on the source buffer's identity and
+        # version counter, so load_state_dict / copy_ into packed_weights (or a
+        # new tensor assigned to it) rebuilds it.
+        src = self.packed_weights
+        key = (src.data_ptr(), src._version, device)
         kp = self._kernel_packed_weights
-        if kp is None or kp.device != device:
-            kp = rowpacked_to_marlin(self.packed_weights.to(device))
+        if kp is None or getattr(self, "_kernel_key", None) != key:
+            kp = rowpacked_to_marlin(src.to(device))
             self._kernel_packed_weights = kp
+            self._kernel_key = key
         return kp
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
@@ -133,8 +130,15 @@ class MMFP4Linear(nn.Module):
         if not x.is_floating_point():
             raise ValueError(f"x must be a floating tensor, got dtype={x.dtype}")
         x2 = x.reshape(-1, self.in_features)
-        out = kernels.marlin_gemm_fp4(x2, self._kernel_weights(x.device),
-                                      self.scales.to(x.device), self.group_size)
+        scales = self.scales.to(x.device)
+        if kernels.rowpacked_gemm_supported(x2.shape[0], self.out_features, self.in_features,
+                                            self.group_size):
+            # decode sizes: row-packed words and [n_groups, out] scales in place
+            out = kernels.mmfp4_gemm_rowpacked(x2, self.packed_weights.to(x.device), scales,
+                                               self.group_size)
+        else:
+            out = kernels.marlin_gemm_fp4(x2, self._kernel_weights(x.device), scales,
+                                          self.group_size)
         if self.bias is not None:
             out = out + self.bias.to(device=out.device, dtype=out.dtype)
         out = out.reshape(*x.shape[:-1], self.out_features)

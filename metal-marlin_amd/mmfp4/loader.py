@@ -1,12 +1,33 @@
-"""On-disk format for FP4 checkpoints: safetensors with the packed weight
-under `name` and its scales under `name.scales` (plus optional
-`.group_size` / `.quant_type` / `.hadamard_block_size` metadata), and the
-converter that writes it.
+"""On-disk format for FP4 checkpoints and the converter that writes it.
 
-Reference: metal_marlin/quantized_loader.py:30-220 (QuantizedModel.load and
-its helpers) and metal_marlin/quantize_fp4.py:399-508
-(load_and_quantize_safetensors, convert_safetensors_to_fp4).  Files are read
-with safetensors (no pickle).  Quantisation runs on the GPU
+Format (restated here from the reference's writer and reader,
+metal_marlin/quantize_fp4.py:445-508 and metal_marlin/quantized_loader.py:
+30-220):
+
+* a directory holding `model.safetensors` and, optionally,
+  `quantization_config.json` (a JSON object; `group_size` and `format` are
+  the defaults for tensors that carry no sidecar of their own);
+* a quantized matrix is a *record*: its data tensor, stored under the
+  record's name `B` (or `B_quantized`), and sidecar tensors stored under
+  `B<sep><field>` with `<sep>` either "." or "_":
+    - `scales`              (required) fp16 group scales;
+    - `group_size`          a 1-element integer tensor;
+    - `quant_type`          the format name as NUL-padded UTF-8 bytes in a
+                            uint8/int8 tensor (names are lower-cased and
+                            reduced to a canonical form: a leading "marlin_"
+                            is dropped, and fp4_e2m1 / fp8_e4m3 / int4_sym
+                            are fp4 / fp8 / int4);
+    - `hadamard_block_size` its presence marks the record as Hadamard-rotated;
+* a key that names no record and has no sidecar is a plain tensor; bf16 plain
+  tensors (router gates and the like) are reported apart.
+
+The unpacked shape of a record follows from the data and scale shapes: data
+rows equal to scale rows means the codes are packed along each row (row
+packing, [N, K/8] with [N, K/g] scales: shape [N, groups * g]); data rows
+equal to groups * g means unpacked rows; otherwise the last axis holds
+`codes per word` codes (8, or 16 for int2).
+
+Files are read with safetensors (no pickle).  Quantisation runs on the GPU
 (`quantize_fp4`), so the converter needs a ROCm device; loading does not.
 """
 
@@ -14,6 +35,7 @@ from __future__ import annotations
 
 import json
 import logging
+import re
 from collections.abc import Iterator
 from dataclasses import dataclass, field
 from pathlib import Path
@@ -29,62 +51,59 @@ __all__ = ["QuantizedModel", "load_and_quantize_safetensors", "convert_safetenso
 
 logger = logging.getLogger(__name__)
 
-_META_SUFFIXES = (".scales", "_scales", ".group_size", "_group_size", ".quant_type",
-                  "_quant_type", ".hadamard_block_size", "_hadamard_block_size")
+# `<record><sep><field>` for every sidecar field of the format
+_SIDECAR_KEY = re.compile(r"^(?P<record>.+)[._](?P<field>scales|group_size|quant_type|"
+                          r"hadamard_block_size)$")
+_DATA_MARK = "_quantized"
+_CANONICAL_FORMAT = {"fp4_e2m1": "fp4", "fp8_e4m3": "fp8", "int4_sym": "int4"}
+_CODES_PER_WORD = {"int2": 16}
+_DEFAULT_CODES_PER_WORD = 8
 
 
-def _strip(name: str, suffix: str) -> str:
-    return name[: -len(suffix)]
+@dataclass
+class _Record:
+    """Sidecars of one quantized matrix, gathered from the key scan."""
+    scales: torch.Tensor | None = None
+    group_size: torch.Tensor | None = None
+    quant_type: str | None = None
+    hadamard: bool = False
+    data: torch.Tensor | None = None
 
 
-def _decode_quant_type(tensor: torch.Tensor) -> str | None:
-    """A uint8/int8 tensor holding a UTF-8 format name (NUL padded)."""
-    if tensor.numel() == 0 or tensor.dtype not in (torch.uint8, torch.int8):
+def _format_name(t: torch.Tensor) -> str | None:
+    """Text of a `quant_type` sidecar (None when it holds no name)."""
+    if t.dtype not in (torch.uint8, torch.int8) or t.numel() == 0:
         return None
-    raw = bytes(tensor.flatten().to(torch.uint8).tolist()).strip(b"\x00")
-    if not raw:
-        return None
-    try:
-        return raw.decode("utf-8").strip()
-    except UnicodeDecodeError:
-        return raw.decode("latin-1", errors="ignore").strip()
+    text = t.reshape(-1).to(torch.uint8).numpy().tobytes().replace(b"\x00", b"")
+    name = text.decode("utf-8", errors="ignore").strip()
+    return name or None
 
 
-def _get_group_size(tensor: torch.Tensor | None, config: dict[str, Any]) -> int:
-    if tensor is not None and tensor.numel() > 0:
-        return int(tensor.reshape(-1)[0].item())
-    return int(config.get("group_size", 0))
+def _canonical_format(name: str | None) -> str:
+    name = (name or "fp4").lower()
+    name = name.removeprefix("marlin_")
+    return _CANONICAL_FORMAT.get(name, name)
 
 
-def _normalize_format(fmt: str | None) -> str:
-    if not fmt:
-        return "fp4"
-    fmt = fmt.lower()
-    if fmt.startswith("marlin_"):
-        fmt = fmt[len("marlin_"):]
-    return {"fp4_e2m1": "fp4", "fp8_e4m3": "fp8", "int4_sym": "int4"}.get(fmt, fmt)
-
-
-def _infer_original_shape(data: torch.Tensor, scales: torch.Tensor | None, group_size: int,
-                          fmt: str) -> tuple[int, ...]:
-    """Unpacked [rows, cols] of a packed weight, from its scales when they
-    pin it, else from the packing factor (8 codes per word; 16 for int2)."""
-    if scales is not None and scales.dim() == 2 and group_size > 0:
-        if scales.shape[0] == data.shape[0]:
-            return (int(scales.shape[0]), int(scales.shape[1]) * group_size)
-        if scales.shape[0] * group_size == data.shape[0]:
-            return (int(scales.shape[0]) * group_size, int(scales.shape[1]))
-    pack = 16 if fmt == "int2" else 8
-    if data.dim() >= 2:
-        return (int(data.shape[0]), int(data.shape[1]) * pack)
-    return (int(data.numel()) * pack,)
+def _unpacked_shape(data: torch.Tensor, scales: torch.Tensor, group_size: int,
+                    fmt: str) -> tuple[int, ...]:
+    if scales.dim() == 2 and group_size > 0:
+        groups, cols = int(scales.shape[0]), int(scales.shape[1])
+        if data.shape[0] == groups:              # row packing: [N, K/8], scales [N, K/g]
+            return (groups, cols * group_size)
+        if data.shape[0] == groups * group_size:  # unpacked rows
+            return (groups * group_size, cols)
+    per_word = _CODES_PER_WORD.get(fmt, _DEFAULT_CODES_PER_WORD)
+    if data.dim() < 2:
+        return (int(data.numel()) * per_word,)
+    return (int(data.shape[0]), int(data.shape[1]) * per_word)
 
 
 @dataclass
 class QuantizedModel:
-    """A quantized checkpoint: `weights` maps base names to QuantizedTensor
-    (or plain tensors), `bf16_weights` holds bf16 tensors kept as they are
-    (router gates and the like)."""
+    """A quantized checkpoint: `weights` maps record names to QuantizedTensor
+    (and plain tensors to themselves), `bf16_weights` holds bf16 plain
+    tensors (router gates and the like)."""
 
     config: dict[str, Any]
     weights: dict[str, QuantizedTensor | torch.Tensor]
@@ -92,59 +111,64 @@ class QuantizedModel:
 
     @classmethod
     def load(cls, path: Path | str) -> "QuantizedModel":
-        """Load `model.safetensors` (+ optional `quantization_config.json`)
-        from the directory `path` (quantized_loader.py:38-138)."""
+        """Read the checkpoint directory `path` (the format above; the
+        reference reader is quantized_loader.py:38-138)."""
         from safetensors.torch import load_file
 
         path = Path(path)
-        weights_path = path / "model.safetensors"
-        if not weights_path.exists():
+        st_file = path / "model.safetensors"
+        if not st_file.exists():
             raise FileNotFoundError(f"model.safetensors not found in {path}")
-        config_path = path / "quantization_config.json"
-        config = json.loads(config_path.read_text()) if config_path.exists() else {}
-        tensors = load_file(str(weights_path))
+        cfg_file = path / "quantization_config.json"
+        config = json.loads(cfg_file.read_text()) if cfg_file.exists() else {}
+        tensors = load_file(str(st_file))
 
-        scales_map: dict[str, torch.Tensor] = {}
-        group_map: dict[str, torch.Tensor] = {}
-        qtype_map: dict[str, str] = {}
-        hadamard_map: dict[str, torch.Tensor] = {}
-        for name, t in tensors.items():
-            for sep in (".", "_"):
-                if name.endswith(f"{sep}scales"):
-                    scales_map[_strip(name, f"{sep}scales")] = t
-                elif name.endswith(f"{sep}group_size"):
-                    group_map[_strip(name, f"{sep}group_size")] = t
-                elif name.endswith(f"{sep}quant_type"):
-                    q = _decode_quant_type(t)
-                    if q is not None:
-                        qtype_map[_strip(name, f"{sep}quant_type")] = q
-                elif name.endswith(f"{sep}hadamard_block_size"):
-                    hadamard_map[_strip(name, f"{sep}hadamard_block_size")] = t
+        # Pass 1: sidecars, keyed by record name.
+        records: dict[str, _Record] = {}
+        plain: list[str] = []
+        for key, t in tensors.items():
+            m = _SIDECAR_KEY.match(key)
+            if m is None:
+                plain.append(key)
+                continue
+            rec = records.setdefault(m["record"], _Record())
+            fld = m["field"]
+            if fld == "scales":
+                rec.scales = t
+            elif fld == "group_size":
+                rec.group_size = t
+            elif fld == "quant_type":
+                rec.quant_type = _format_name(t)
+            else:
+                rec.hadamard = True
 
+        # Pass 2: data tensors; a data key names a record when it carries the
+        # `_quantized` mark or when sidecars were stored under its name.
         weights: dict[str, QuantizedTensor | torch.Tensor] = {}
         bf16: dict[str, torch.Tensor] = {}
-        for name, t in tensors.items():
-            if name.endswith(_META_SUFFIXES):
+        for key in plain:
+            t = tensors[key]
+            marked = key.endswith(_DATA_MARK)
+            name = key[: -len(_DATA_MARK)] if marked else key
+            rec = records.get(name)
+            if rec is not None and rec.quant_type is None and rec.scales is None \
+                    and rec.group_size is None and not rec.hadamard:
+                rec = None   # a quant_type sidecar that held no name
+            if rec is None and not marked:
+                (bf16 if t.dtype == torch.bfloat16 else weights)[name] = t
                 continue
-            base = name[:-len("_quantized")] if name.endswith("_quantized") else name
-            quantized = (base in scales_map or base in group_map or base in qtype_map
-                         or base in hadamard_map or name.endswith("_quantized"))
-            if quantized:
-                if base in weights or base in bf16:
-                    continue
-                scales = scales_map.get(base)
-                if scales is None:
-                    raise ValueError(f"Missing scales for quantized weight: {base}")
-                gs = _get_group_size(group_map.get(base), config)
-                fmt = _normalize_format(qtype_map.get(base) or config.get("format"))
-                weights[base] = QuantizedTensor(
-                    data=t, scales=scales, format=fmt, group_size=gs,
-                    original_shape=_infer_original_shape(t, scales, gs, fmt),
-                    needs_hadamard=base in hadamard_map, hadamard_matrix=None)
-            elif t.dtype == torch.bfloat16:
-                bf16[base] = t
-            else:
-                weights[base] = t
+            if name in weights or name in bf16:
+                continue     # first data key of a record wins
+            rec = rec or _Record()
+            if rec.scales is None:
+                raise ValueError(f"Missing scales for quantized weight: {name}")
+            gs = (int(rec.group_size.reshape(-1)[0].item()) if rec.group_size is not None
+                  and rec.group_size.numel() > 0 else int(config.get("group_size", 0)))
+            fmt = _canonical_format(rec.quant_type or config.get("format"))
+            weights[name] = QuantizedTensor(
+                data=t, scales=rec.scales, format=fmt, group_size=gs,
+                original_shape=_unpacked_shape(t, rec.scales, gs, fmt),
+                needs_hadamard=rec.hadamard, hadamard_matrix=None)
         return cls(config=config, weights=weights, bf16_weights=bf16)
 
 

@@ -75,10 +75,11 @@ def test_dispatch_gemm_fp4_and_gemmfp4(rng):
                                      (1, 4096, 28672, 128), (3, 2048, 1028, 64),
                                      (2, 4096, 6144, 128), (8, 1024, 3072, 64), (5, 4608, 4100, 128)])
 def test_rowpacked_gemm_in_place(M, K, N, g):
-    """mm_fp4_gemm_rowpacked reads [N, K/8] words and [N, K/g] scales in place
+    """mm_fp4_gemm_rowpacked reads [N, K/8] words and the scales in place, in
+    either layout the layer accepts ([K/g, N] canonical, [N, K/g] transposed)
     (layers/mmfp4_linear.py:549-598 without its per-call transpose): parity
     with the fp32 reference of the same weights, including the split-K shape
-    14336 -> 4096."""
+    14336 -> 4096.  Both scale layouts give bit-identical results."""
     import mmfp4
     gen = torch.Generator(device="cuda").manual_seed(M * 3 + K + N)
     w = (torch.randn((N, K), generator=gen, device="cuda") * 0.02).half()
@@ -89,9 +90,12 @@ def test_rowpacked_gemm_in_place(M, K, N, g):
     announce(f"row-packed gemm M={M} K={K} N={N} g={g}")
     out = mmfp4.mmfp4_gemm_rowpacked(a, rows, srows, g)
     assert max_abs_rel(to_np(out), to_np(ref)) <= TOL
+    out_g = mmfp4.mmfp4_gemm_rowpacked(a, rows, scales, g)
+    assert torch.equal(out_g.view(torch.int16), out.view(torch.int16))
     # the layer-level functional entry takes this path and agrees
-    fn = mmfp4.layers.mmfp4_gemm(a, rows, srows, g)
-    assert torch.equal(fn.view(torch.int16), out.view(torch.int16))
+    for sc in (srows, scales):
+        fn = mmfp4.layers.mmfp4_gemm(a, rows, sc, g)
+        assert torch.equal(fn.view(torch.int16), out.view(torch.int16))
 
 
 def test_rowpacked_gemm_refuses_unsupported_shapes():
@@ -110,23 +114,74 @@ def test_rowpacked_gemm_refuses_unsupported_shapes():
 
 @pytest.mark.parametrize("M,K,N,g", [(1, 4096, 4096, 128), (8, 14336, 4096, 128),
                                      (16, 512, 100, 32), (3, 4096, 6144, 64),
-                                     (40, 512, 256, 128)])
-def test_kernels_mmfp4_gemm_scales_in_place(M, K, N, g):
-    """kernels.mmfp4_gemm (kernels_core.py:4804-4812): Marlin-layout words with
-    the MMFP4 kernel's [N, K/g] scales.  Decode sizes read the scales in place
-    (mm_fp4_gemm_mmfp4); M > 16 transposes them.  Parity with the fp32
-    reference."""
+                                     (40, 512, 256, 128), (1, 1024, 8, 128), (24, 2048, 16, 128)])
+def test_kernels_mmfp4_gemm_scale_layouts(M, K, N, g):
+    """kernels.mmfp4_gemm (kernels_core.py:4804-4812 -> MetalKernels.mmfp4_gemm
+    :4550-4633): Marlin-layout words with [K/g, N] scales, the layout the
+    reference kernel reads (shaders/mmfp4_gemm.metal:570-588).  [N, K/g]
+    scales are accepted when the shape is unambiguous (read in place at decode
+    sizes, transposed above); a square tensor (N == K/g: the (1, 1024, 8) and
+    (24, 2048, 16) cases) is read as [K/g, N].  Parity with the fp32
+    reference, and dequantize_mmfp4 bit-exact with dequant_fp4."""
     import mmfp4
     gen = torch.Generator(device="cuda").manual_seed(M + 5 * K + N)
     w = (torch.randn((N, K), generator=gen, device="cuda") * 0.02).half()
     a = torch.randn((M, K), generator=gen, device="cuda").half()
     p, s = mmfp4.quantize_fp4(w, group_size=g)
-    ref = a.float() @ mmfp4.dequant_fp4(p, s, K, N, g).float()
+    deq = mmfp4.dequant_fp4(p, s, K, N, g)
+    ref = a.float() @ deq.float()
     announce(f"kernels.mmfp4_gemm M={M} K={K} N={N} g={g}")
-    out = mmfp4.mmfp4_gemm(a, p, s.t().contiguous(), g)
+    out = mmfp4.mmfp4_gemm(a, p, s, g)
     assert out.shape == (M, N)
     assert max_abs_rel(to_np(out), to_np(ref)) <= TOL
-    if M <= 8 and K * N <= 4096 * 6144:
-        # The two-slab decode kernel serves both scale layouts with the same
-        # summation order: the results must agree bit for bit.
-        assert torch.equal(out, mmfp4.marlin_gemm_fp4(a, p, s, g))
+    assert torch.equal(out, mmfp4.marlin_gemm_fp4(a, p, s, g))
+    assert torch.equal(mmfp4.dequantize_mmfp4(p, s, g).view(torch.int16), deq.view(torch.int16))
+    if N != K // g:
+        st = s.t().contiguous()
+        out_t = mmfp4.mmfp4_gemm(a, p, st, g)
+        assert max_abs_rel(to_np(out_t), to_np(ref)) <= TOL
+        assert torch.equal(mmfp4.dequantize_mmfp4(p, st, g).view(torch.int16),
+                           deq.view(torch.int16))
+        if M <= 8 and K * N <= 4096 * 6144:
+            # The two-slab decode kernel serves both scale layouts with the same
+            # summation order: the results must agree bit for bit.
+            assert torch.equal(out_t, out)
+    else:
+        # square: read as [K/g, N]; the transposed tensor is a different matrix
+        other = mmfp4.mmfp4_gemm(a, p, s.t().contiguous(), g)
+        ref_t = a.float() @ mmfp4.dequant_fp4(p, s.t().contiguous(), K, N, g).float()
+        assert max_abs_rel(to_np(other), to_np(ref_t)) <= TOL
+
+
+def test_mmfp4_gemm_rejects_mismatched_scales():
+    import mmfp4
+    a = torch.zeros((1, 512), dtype=torch.float16, device="cuda")
+    p = torch.zeros((64, 96), dtype=torch.int32, device="cuda")
+    with pytest.raises(ValueError, match="neither"):
+        mmfp4.mmfp4_gemm(a, p, torch.ones((5, 96), dtype=torch.float16, device="cuda"), 128)
+
+
+def test_mmfp4_linear_reloaded_weights_take_effect(rng):
+    """MMFP4Linear's Marlin-layout copy (used at M > 16) follows writes to
+    packed_weights: load_state_dict with new weights changes the output at
+    every M, and matches the oracle of the new weights."""
+    import mmfp4
+    out_f, in_f, g = 256, 512, 128
+    w1 = rng.normal(0, 0.02, (out_f, in_f)).astype(np.float16)
+    w2 = rng.normal(0, 0.02, (out_f, in_f)).astype(np.float16)
+    m1, s1 = ofp4.quantize_fp4(w1, g)
+    m2, s2 = ofp4.quantize_fp4(w2, g)
+    layer = mmfp4.MMFP4Linear(to_dev(np.ascontiguousarray(m1.T).view(np.int32)), to_dev(s1),
+                              None, g)
+    for M in (1, 40):
+        x = rng.normal(0, 1, (M, in_f)).astype(np.float16)
+        announce(f"MMFP4Linear reload M={M}")
+        y1 = layer(to_dev(x))
+        assert max_abs_rel(to_np(y1), ofp4.gemm_fp4_ref(x, m1, s1, g)) <= TOL
+        sd = {"packed_weights": to_dev(np.ascontiguousarray(m2.T).view(np.int32)),
+              "scales": to_dev(s2)}
+        layer.load_state_dict(sd, strict=False)
+        y2 = layer(to_dev(x))
+        assert max_abs_rel(to_np(y2), ofp4.gemm_fp4_ref(x, m2, s2, g)) <= TOL
+        layer.load_state_dict({"packed_weights": to_dev(np.ascontiguousarray(m1.T).view(np.int32)),
+                               "scales": to_dev(s1)}, strict=False)

@@ -96,3 +96,30 @@ def test_convert_then_load_then_gemm(tmp_path):
     out = mmfp4.marlin_gemm_fp4(to_dev(x), q.data.cuda(), q.scales.cuda(), g)
     assert max_abs_rel(to_np(out), ofp4.gemm_fp4_ref(x, op, os_, g)) <= TOL
     assert np.array_equal(m.weights["odd.weight"].numpy(), src["odd.weight"])
+
+
+def test_quantized_model_format_names_and_packing(tmp_path):
+    """Format-name sidecars (NUL padding, marlin_ prefix, aliases, empty), the
+    config defaults, and the codes-per-word rule of the unpacked shape."""
+    import mmfp4
+    words = torch.zeros((4, 6), dtype=torch.int32)
+    name = lambda b: torch.tensor(list(b), dtype=torch.uint8)
+    t = {
+        "i2.weight": words.clone(), "i2.weight.scales": torch.ones((3, 5)).half(),
+        "i2.weight.quant_type": name(b"int2\x00"),
+        "s.weight": words.clone(), "s.weight_scales": torch.ones((3, 5)).half(),
+        "s.weight_quant_type": name(b"MARLIN_INT4_SYM"),
+        "d.weight": words.clone(), "d.weight.scales": torch.ones((3, 5)).half(),
+        "e.weight": words.clone(), "e.weight.quant_type": name(b"\x00\x00"),
+    }
+    save_torch(t, str(tmp_path / "model.safetensors"))
+    (tmp_path / "quantization_config.json").write_text(json.dumps({"group_size": 64,
+                                                                   "format": "fp8_e4m3"}))
+    m = mmfp4.QuantizedModel.load(tmp_path)
+    assert m.weights["i2.weight"].format == "int2"
+    assert m.weights["i2.weight"].original_shape == (4, 6 * 16)
+    assert m.weights["s.weight"].format == "int4"
+    assert m.weights["s.weight"].original_shape == (4, 6 * 8)
+    assert m.weights["d.weight"].format == "fp8" and m.weights["d.weight"].group_size == 64
+    # a format sidecar with no name marks nothing: e.weight is a plain tensor
+    assert torch.equal(m.weights["e.weight"], t["e.weight"])
