@@ -221,6 +221,28 @@ int mm_moe_mlp_fp4(const uint16_t* X, const void* expert_ids, int ids_i64, const
                    const uint32_t* Bdn, const uint16_t* Sdn, int group_size, uint16_t* act_buf,
                    uint16_t* y_buf, int32_t* sort_buf, uint16_t* out, void* stream);
 
+/* ------------------------------------------- flat-group FP4 (FP4Metal) */
+
+/* Quantizes n values (dtype 0 f32, 1 fp16, 2 bf16) in flat groups of
+ * group_size over the flattened tensor, the last group padded with zeros:
+ * scales[i] = max(max|x| / 6, 1e-8) in f32 (NaN when the group holds a NaN),
+ * codes[j] = (v < 0 ? 8 : 0) | nearest positive E2M1 index of |v| (ties to the
+ * lower index) for v = x[j] / scales[j / group_size].  codes: n bytes;
+ * scales: ceil(n / group_size) floats.  Replaces metal_marlin/fp4_metal.py:
+ * 130-190 (FP4Metal.quantize). */
+int mm_fp4_flat_quantize(const void* x, size_t n, int dtype, int group_size, uint8_t* codes,
+                         float* scales, void* stream);
+
+/* out[j] = E2M1[codes[j] & 15] * scales[j / group_size] in f32; requires
+ * nscales * group_size >= n.  Replaces metal_marlin/fp4_metal.py:192-276
+ * (FP4Metal.dequantize). */
+int mm_fp4_flat_dequantize(const uint8_t* codes, const float* scales, size_t n, size_t nscales,
+                           int group_size, float* out, void* stream);
+
+/* out[j] = (lo[j] & 15) | ((hi[j] & 15) << 4).  Replaces
+ * metal_marlin/fp4_metal.py:278-300 (FP4Metal.pack_pair). */
+int mm_fp4_pack_pair(const uint8_t* lo, const uint8_t* hi, size_t n, uint8_t* out, void* stream);
+
 /* ------------------------------------------------------------ measurement */
 
 /* Reads `bytes` (a multiple of 16, 16-byte aligned) of device memory once

@@ -30,7 +30,7 @@ COMMON = [
 ]
 # Per-file extra flags: the quantizers reproduce numpy's float32 arithmetic
 # operation by operation, so no contraction there.
-EXTRA = {"mm_quant.hip": ["-ffp-contract=off"]}
+EXTRA = {"mm_quant.hip": ["-ffp-contract=off"], "mm_fp4flat.hip": ["-ffp-contract=off"]}
 
 
 def hipcc() -> str:

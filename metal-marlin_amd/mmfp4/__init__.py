@@ -11,6 +11,7 @@ from .kernels import (FP4_PER_UINT, decode_gemv_fp4, dequant_fp4, dequant_fp4_de
                       select_decode_kernel)
 from .gpu_grouping import (GPUExpertGrouping, GPUGroupingResult, group_tokens_by_expert_auto,
                            group_tokens_by_expert_fast, group_tokens_by_expert_gpu_optimized)
+from .fp4_metal import FP4Metal, dequantize_fp4_metal, quantize_fp4_metal
 from .layers import MMFP4Linear
 from .ops import GemmFp4, dispatch_gemm_fp4
 from .loader import QuantizedModel, convert_safetensors_to_fp4, load_and_quantize_safetensors

@@ -25,6 +25,11 @@ Pinning status (what checks each function against something other than itself):
   ties of w/s + z and of -min/s (half-to-even), and one-signed groups whose
   zero point lies outside [0, 15] and is stored unclipped; also the round-trip
   bound and the reference test-file quantizer on clip-free inputs.
+* `flat_quantize`, `flat_dequantize`, `pack_pair` (FP4Metal) -- pinned
+  (tests/test_oracle_flat.py): nearest-E2M1 brute force in float64 with ties
+  to the lower index, sign from v < 0 (so -0.0 -> code 0), the scale closed
+  form and its 1e-8 floor, zero padding of the last group, NaN/inf groups,
+  and hand-computed known answers.
 * `gemm_fp4_ref`, `gemm_u4_ref`  -- fp32 dequant+matmul; pinned by the
   zero / linearity / all-ones-large-K closed forms of tests/test_gemm.py and a
   brute-force float64 triple loop on tiny shapes.

@@ -187,3 +187,48 @@ def max_abs_rel(out: np.ndarray, ref: np.ndarray) -> float:
     ref = np.asarray(ref, dtype=np.float64)
     denom = max(float(np.max(np.abs(ref))), 1e-30)
     return float(np.max(np.abs(out - ref))) / denom
+
+
+# ---------------------------------------------------------------------------
+# Flat-group FP4 (FP4Metal, metal_marlin/fp4_metal.py:130-300)
+# ---------------------------------------------------------------------------
+def flat_quantize(values: np.ndarray, group_size: int = 128):
+    """FP4Metal.quantize (fp4_metal.py:130-190): flatten to float32, pad the
+    last group with zeros (:150-160), scales = max(max|x| / 6, 1e-8) in f32
+    (:161-163), v = x / scale (:166), code = (8 if v < 0 else 0) | argmin_j
+    |E2M1_POS[j] - |v|| (:167-172, ties to the lower j).  Returns (codes
+    uint8 in the input's shape, scales float32 [n_groups])."""
+    v = np.asarray(values)
+    flat = v.reshape(-1).astype(np.float32)
+    n = flat.shape[0]
+    n_groups = (n + group_size - 1) // group_size
+    padded = np.zeros(n_groups * group_size, np.float32)
+    padded[:n] = flat
+    g = padded.reshape(n_groups, group_size)
+    with np.errstate(invalid="ignore", divide="ignore"):
+        scales = np.maximum(np.max(np.abs(g), axis=1) / np.float32(6.0), np.float32(1e-8))
+        normalized = (g / scales[:, None]).reshape(-1)
+        dist = np.abs(_E2M1_POS[None, :] - np.abs(normalized)[:, None])
+    pos_idx = np.argmin(dist, axis=1).astype(np.uint8)        # all-NaN rows -> 0
+    sign = np.where(normalized < 0, np.uint8(8), np.uint8(0))
+    codes = (sign | pos_idx)[:n].reshape(v.shape)
+    return codes, scales.astype(np.float32)
+
+
+def flat_dequantize(codes: np.ndarray, scales: np.ndarray, group_size: int = 128) -> np.ndarray:
+    """FP4Metal.dequantize (fp4_metal.py:192-276): E2M1[code] * scale in
+    float32, groups over the flattened codes; shape of `codes`."""
+    c = np.asarray(codes)
+    s = np.asarray(scales, dtype=np.float32).reshape(-1)
+    flat = E2M1_VALUES[c.reshape(-1).astype(np.int64)]
+    n = flat.shape[0]
+    padded = np.zeros(s.shape[0] * group_size, np.float32)
+    padded[:n] = flat
+    return (padded.reshape(-1, group_size) * s[:, None]).reshape(-1)[:n].reshape(c.shape)
+
+
+def pack_pair(lo: np.ndarray, hi: np.ndarray) -> np.ndarray:
+    """FP4Metal.pack_pair (fp4_metal.py:278-300): (lo & 15) | ((hi & 15) << 4)."""
+    lo = np.asarray(lo, dtype=np.uint8)
+    hi = np.asarray(hi, dtype=np.uint8)
+    return (lo & np.uint8(0x0F)) | ((hi & np.uint8(0x0F)) << np.uint8(4))
