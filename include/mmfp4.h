@@ -221,6 +221,26 @@ int mm_moe_mlp_fp4(const uint16_t* X, const void* expert_ids, int ids_i64, const
                    const uint32_t* Bdn, const uint16_t* Sdn, int group_size, uint16_t* act_buf,
                    uint16_t* y_buf, int32_t* sort_buf, uint16_t* out, void* stream);
 
+/* mm_moe_mlp_fp4 plus a shared expert that every token visits:
+ *   out[t] = base[t] + sum_j probs[t, j] * y_routed(t, j) + shared_weight * y_shared(t)
+ * with y_shared(t) = (silu(h[:I]) * h[I:]) . W_sdn, h = X[t] . W_sgu, W_sgu
+ * [H/8, 2I] packed (scales [H/g, 2I]), W_sdn [I/8, H] (scales [I/g, H]).  The
+ * shared expert runs as one more expert group in the same two grouped
+ * launches as the routed experts.  k may be 0 (shared expert alone: E may
+ * then be 0, and expert_ids, probs and the routed weights may be NULL);
+ * base (fp16 [T, H]) may be NULL.  Scratch: act_buf fp16 [T*(k+1), I], y_buf
+ * fp16 [T*(k+1), H], sort_buf int32 [E + 2 + 2*T*(k+1)].  Replaces
+ * metal_marlin/kernels/moe.py:742-856 (moe_fused_dispatch_shared_fp4),
+ * :442-582 (moe_shared_expert_fp4), :858-930 (moe_add_shared_expert_fp4) and
+ * the forward of metal_marlin/moe_dispatch.py:1111-1238 (FusedMoEDispatcher). */
+int mm_moe_mlp_shared_fp4(const uint16_t* X, const void* expert_ids, int ids_i64,
+                          const float* probs, int T, int k, int E, int H, int I,
+                          const uint32_t* Bgu, const uint16_t* Sgu, const uint32_t* Bdn,
+                          const uint16_t* Sdn, const uint32_t* Bsgu, const uint16_t* Ssgu,
+                          const uint32_t* Bsdn, const uint16_t* Ssdn, float shared_weight,
+                          const uint16_t* base, int group_size, uint16_t* act_buf,
+                          uint16_t* y_buf, int32_t* sort_buf, uint16_t* out, void* stream);
+
 /* ------------------------------------------- flat-group FP4 (FP4Metal) */
 
 /* Quantizes n values (dtype 0 f32, 1 fp16, 2 bf16) in flat groups of

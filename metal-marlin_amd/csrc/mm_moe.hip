@@ -31,6 +31,23 @@ using namespace mmpf;
 #define MM_MOE_PF_ROWS 24   // average rows per expert above which the MFMA tile kernel runs
 #endif
 
+// Expert weights: experts e < Er are slices of the stacked [Er, K/8, N]
+// words and [Er, K/g, N] scales; expert Er (when a shared expert is run as an
+// extra group) has its own [K/8, N] / [K/g, N] tensors.
+struct ExpertW {
+  const uint32_t* B;
+  const f16* S;
+  const uint32_t* Bsh;
+  const f16* Ssh;
+  int Er;
+  MM_DEV const uint32_t* b(int e, int K, int N) const {
+    return e < Er ? B + (size_t)e * (K / 8) * N : Bsh;
+  }
+  MM_DEV const f16* s(int e, int K, int N, int g) const {
+    return e < Er ? S + (size_t)e * (K / g) * N : Ssh;
+  }
+};
+
 constexpr int SORT_THREADS = 1024;
 constexpr int MOE_MAX_EXPERTS = SORT_THREADS;   // the sort holds one expert per thread
 constexpr int SORT_WAVES = SORT_THREADS / 64;
@@ -45,9 +62,12 @@ constexpr int SORT_KC = 8;          // 64-key chunks fetched together per wave
 // expert offsets and each wave's first position per expert; pass 2 places
 // every assignment at its wave's running position plus its rank among the
 // equal lanes below it.  Dynamic LDS: wpos[SORT_WAVES][E] ints.
-template <typename IdT>
+// SH: every token has one more slot (index kin of kin + 1) whose key is the
+// shared-expert group E - 1; n = T * (kin + 1) then, and flat indices run
+// over the kin + 1 slots.
+template <typename IdT, bool SH>
 __global__ void __launch_bounds__(SORT_THREADS)
-k_moe_sort(const IdT* __restrict__ ids, int n, int E, int32_t* __restrict__ offsets,
+k_moe_sort(const IdT* __restrict__ ids, int n, int E, int kin, int32_t* __restrict__ offsets,
            int32_t* __restrict__ sorted_idx, int32_t* __restrict__ inverse) {
   extern __shared__ int wpos[];
   __shared__ int wsum[SORT_WAVES];
@@ -64,8 +84,15 @@ k_moe_sort(const IdT* __restrict__ ids, int n, int E, int32_t* __restrict__ offs
   // Keys past the segment read a clamped index (the load is unconditional, so
   // the SORT_KC loads of a batch stay in flight together) and become -1.
   auto key_at = [&](int i) {
-    const long long v = (long long)ids[min(i, n - 1)];
-    return (i < seg1 && v >= 0 && v < E) ? (int)v : -1;
+    if constexpr (SH) {
+      const int t = i / (kin + 1), j = i - t * (kin + 1);
+      if (j == kin) return i < seg1 ? E - 1 : -1;
+      const long long v = (long long)ids[min(t * kin + j, n / (kin + 1) * kin - 1)];
+      return (i < seg1 && v >= 0 && v < E - 1) ? (int)v : -1;
+    } else {
+      const long long v = (long long)ids[min(i, n - 1)];
+      return (i < seg1 && v >= 0 && v < E) ? (int)v : -1;
+    }
   };
   auto match = [&](int key) {
     const bool valid = key >= 0;
@@ -172,9 +199,8 @@ k_moe_sort(const IdT* __restrict__ ids, int n, int E, int32_t* __restrict__ offs
 template <int MT, int NW, int SPW, int FL>
 __global__ void __launch_bounds__(NW * 64)
 k_moe_grouped(const f16* __restrict__ X, const int32_t* __restrict__ sorted_idx,
-              const int32_t* __restrict__ offsets, int gather, int topk,
-              const uint32_t* __restrict__ Ball, const f16* __restrict__ Sall, int K, int N,
-              int g, int act, f16* __restrict__ Y) {
+              const int32_t* __restrict__ offsets, int gather, int topk, ExpertW W, int K,
+              int N, int g, int act, f16* __restrict__ Y) {
   constexpr int NT = 2;
   constexpr int MOE_NW = NW, MOE_SPW = SPW;
   __shared__ float red[(MOE_NW - 1) * MT * NT * 16 * 64];
@@ -183,8 +209,8 @@ k_moe_grouped(const f16* __restrict__ X, const int32_t* __restrict__ sorted_idx,
   if (r1 <= r0) return;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int c = lane & 15, q = lane >> 4;
-  const uint32_t* B = Ball + (size_t)e * (K / 8) * N;
-  const f16* S = Sall + (size_t)e * (K / g) * N;
+  const uint32_t* B = W.b(e, K, N);
+  const f16* S = W.s(e, K, N, g);
   const int nout = act ? N / 2 : N;
   const int n0 = act ? blockIdx.x * SK_COLS : blockIdx.x * NT * SK_COLS;
   const int coloff = act ? N / 2 : SK_COLS;
@@ -279,9 +305,8 @@ struct MoeSrc {
 template <int WM, int WN, int RB, bool G64, int STAGES>
 __global__ void __launch_bounds__(WM * WN * 64)
 k_moe_prefill(const f16* __restrict__ X, const int32_t* __restrict__ sorted_idx,
-              const int32_t* __restrict__ offsets, int gather, int topk,
-              const uint32_t* __restrict__ Ball, const f16* __restrict__ Sall, int E, int K,
-              int N, int g, int act, int gx, f16* __restrict__ Y) {
+              const int32_t* __restrict__ offsets, int gather, int topk, ExpertW W, int E,
+              int K, int N, int g, int act, int gx, f16* __restrict__ Y) {
   constexpr int CW = 2;
   constexpr int SROWS = G64 ? PF2_SROWS_G64 : PF2_SROWS;
   using Sh = Pf2Shape<false, WM, WN, RB, CW, STAGES, SROWS>;
@@ -337,7 +362,7 @@ k_moe_prefill(const f16* __restrict__ X, const int32_t* __restrict__ sorted_idx,
   const int half = N / 2;
   const int o0 = act ? bx * (BN / 2) : bx * BN;
   const MoeSrc src{X, sorted_idx, gather, topk, K, mb, r1 - 1, act, half, o0,
-                   Ball + (size_t)e * (K / 8) * N, Sall + (size_t)e * (K / g) * N, nullptr, N};
+                   W.b(e, K, N), W.s(e, K, N, g), nullptr, N};
   const int rb_live =
       __builtin_amdgcn_readfirstlane(min(RB, max(0, (rows - wm * 32 * RB + 31) / 32)));
   f32x16 acc[RB][CW];
@@ -375,16 +400,25 @@ k_moe_prefill(const f16* __restrict__ X, const int32_t* __restrict__ sorted_idx,
   }
 }
 
-// out[t, :] = sum_j probs[t, j] * Y[inverse[t*k + j], :]; one block per token,
-// 8 columns per thread.
+// out[t, :] = base[t, :] + sum_j p_j * Y[inverse[t*k + j], :] with p_j =
+// probs[t, j] for the kin routed slots and p_kin = wsh for the shared slot
+// (k = kin + 1 when a shared expert ran as an extra group, else k = kin);
+// base may be null.  Summed in fp32 in slot order; one block per token, 8
+// columns per thread.
 __global__ void __launch_bounds__(256)
 k_moe_combine(const f16* __restrict__ Y, const float* __restrict__ probs,
-              const int32_t* __restrict__ inverse, int k, int H, f16* __restrict__ out) {
+              const int32_t* __restrict__ inverse, int k, int kin, float wsh,
+              const f16* __restrict__ base, int H, f16* __restrict__ out) {
   const int t = blockIdx.x;
   for (int h8 = threadIdx.x; h8 < H / 8; h8 += 256) {
     float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (base) {
+      const f16x8 b = *(const f16x8*)(base + (size_t)t * H + 8 * h8);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] = (float)b[i];
+    }
     for (int j = 0; j < k; ++j) {
-      const float p = probs[(size_t)t * k + j];
+      const float p = j < kin ? probs[(size_t)t * kin + j] : wsh;
       const f16x8 y = *(const f16x8*)(Y + (size_t)inverse[(size_t)t * k + j] * H + 8 * h8);
 #pragma unroll
       for (int i = 0; i < 8; ++i) acc[i] += p * (float)y[i];
@@ -396,40 +430,33 @@ k_moe_combine(const f16* __restrict__ Y, const float* __restrict__ probs,
   }
 }
 
+// shared: append the shared-expert slot (group E - 1) to every token; the
+// ids are then [T, k] routed ids for the E - 1 routed experts.
 template <typename IdT>
 int moe_sort(const char* who, const IdT* expert_ids, int T, int k, int E, int32_t* offsets,
-             int32_t* sorted_idx, int32_t* inverse, void* stream) {
-  MM_CHECK_ARG(T >= 0 && k > 0, "%s: bad T=%d k=%d", who, T, k);
+             int32_t* sorted_idx, int32_t* inverse, void* stream, bool shared = false) {
+  MM_CHECK_ARG(T >= 0 && (k > 0 || (shared && k == 0)), "%s: bad T=%d k=%d", who, T, k);
   MM_CHECK_ARG(E > 0 && E <= SORT_THREADS, "%s: num_experts=%d must be in [1, %d]", who, E,
                SORT_THREADS);
-  MM_CHECK_ARG((long)T * k < (1L << 30), "%s: T*k too large", who);
+  const int kt = k + (shared ? 1 : 0);
+  MM_CHECK_ARG((long)T * kt < (1L << 30), "%s: T*k too large", who);
   const size_t lds = (size_t)SORT_WAVES * E * sizeof(int);
-  hipLaunchKernelGGL(k_moe_sort<IdT>, dim3(1), dim3(SORT_THREADS), lds, (hipStream_t)stream,
-                     expert_ids, T * k, E, offsets, sorted_idx, inverse);
+  if (shared)
+    hipLaunchKernelGGL((k_moe_sort<IdT, true>), dim3(1), dim3(SORT_THREADS), lds,
+                       (hipStream_t)stream, expert_ids, T * kt, E, k, offsets, sorted_idx,
+                       inverse);
+  else
+    hipLaunchKernelGGL((k_moe_sort<IdT, false>), dim3(1), dim3(SORT_THREADS), lds,
+                       (hipStream_t)stream, expert_ids, T * kt, E, k, offsets, sorted_idx,
+                       inverse);
   MM_CHECK_LAUNCH(who);
   return 0;
 }
 
-}  // namespace
-
-// ===========================================================================
-// C ABI
-// ===========================================================================
-
-extern "C" int mm_moe_sort(const int32_t* expert_ids, int T, int k, int E, int32_t* offsets,
-                           int32_t* sorted_idx, int32_t* inverse, void* stream) {
-  return moe_sort("mm_moe_sort", expert_ids, T, k, E, offsets, sorted_idx, inverse, stream);
-}
-
-extern "C" int mm_moe_sort_i64(const int64_t* expert_ids, int T, int k, int E, int32_t* offsets,
-                               int32_t* sorted_idx, int32_t* inverse, void* stream) {
-  return moe_sort("mm_moe_sort_i64", expert_ids, T, k, E, offsets, sorted_idx, inverse, stream);
-}
-
-extern "C" int mm_moe_grouped_gemm(const uint16_t* X, const int32_t* sorted_idx,
-                                   const int32_t* offsets, int gather, int k, int T,
-                                   const uint32_t* B, const uint16_t* S, int E, int K, int N,
-                                   int g, int act, uint16_t* Y, void* stream) {
+// Grouped expert GEMM over E groups (W: their weights) of k*T sorted rows.
+int grouped_gemm(const uint16_t* X, const int32_t* sorted_idx, const int32_t* offsets,
+                 int gather, int k, int T, ExpertW W, int E, int K, int N, int g, int act,
+                 uint16_t* Y, void* stream) {
   MM_CHECK_ARG(E > 0 && K > 0 && N > 0 && T >= 0 && k > 0, "mm_moe_grouped_gemm: bad shape");
   MM_CHECK_ARG(K % 8 == 0, "mm_moe_grouped_gemm: K=%d must be divisible by 8", K);
   MM_CHECK_ARG(g > 0 && g % 8 == 0 && K % g == 0,
@@ -450,11 +477,7 @@ extern "C" int mm_moe_grouped_gemm(const uint16_t* X, const int32_t* sorted_idx,
     // Row tile: 64 rows while groups average under 48 rows, else 96 (measured
     // on MI355X at the Qwen3-30B-A3B shapes, T = 256..4096: 96-row tiles beat
     // 128 and 256 once per-expert counts vary by tens of rows).
-#ifdef MM_MOE_PF_CFG
-    const int cfg = MM_MOE_PF_CFG;
-#else
     const int cfg = tk < 48L * E ? 1 : 3;
-#endif
 #define MM_LAUNCH_MOE_PF(WM, WN, RB, ST)                                                         \
   do {                                                                                         \
     constexpr int BM = WM * 32 * RB, BN = WN * 64;                                             \
@@ -464,19 +487,16 @@ extern "C" int mm_moe_grouped_gemm(const uint16_t* X, const int32_t* sorted_idx,
     if (g % PF2_BK == 0)                                                                       \
       hipLaunchKernelGGL((k_moe_prefill<WM, WN, RB, true, ST>), dim3((unsigned)blocks), \
                          dim3(WM * WN * 64), 0, (hipStream_t)stream, (const f16*)X, sorted_idx, \
-                         offsets, gather, k, B, (const f16*)S, E, K, N, g, act, gx, (f16*)Y);  \
+                         offsets, gather, k, W, E, K, N, g, act, gx, (f16*)Y);  \
     else                                                                                       \
       hipLaunchKernelGGL((k_moe_prefill<WM, WN, RB, false, ST>), dim3((unsigned)blocks),\
                          dim3(WM * WN * 64), 0, (hipStream_t)stream, (const f16*)X, sorted_idx, \
-                         offsets, gather, k, B, (const f16*)S, E, K, N, g, act, gx, (f16*)Y);  \
+                         offsets, gather, k, W, E, K, N, g, act, gx, (f16*)Y);  \
   } while (0)
-    switch (cfg) {
-      case 0: MM_LAUNCH_MOE_PF(2, 4, 2, 3); break;                  // 128 x 256, 8 waves
-      case 1: MM_LAUNCH_MOE_PF(1, 4, 2, MM_MOE_PF_STAGES); break;   // 64 x 256, 4 waves
-      case 2: MM_LAUNCH_MOE_PF(1, 8, 2, 3); break;                  // 64 x 512, 8 waves
-      case 3: MM_LAUNCH_MOE_PF(1, 4, 3, MM_MOE_PF_STAGES); break;   // 96 x 256, 4 waves
-      default: MM_LAUNCH_MOE_PF(2, 4, 4, 3); break;                 // 256 x 256, 8 waves
-    }
+    if (cfg == 1)
+      MM_LAUNCH_MOE_PF(1, 4, 2, MM_MOE_PF_STAGES);    // 64 x 256, 4 waves
+    else
+      MM_LAUNCH_MOE_PF(1, 4, 3, MM_MOE_PF_STAGES);    // 96 x 256, 4 waves
 #undef MM_LAUNCH_MOE_PF
     MM_CHECK_LAUNCH("mm_moe_grouped_gemm(prefill)");
     return 0;
@@ -488,15 +508,11 @@ extern "C" int mm_moe_grouped_gemm(const uint16_t* X, const int32_t* sorted_idx,
   // each block pulls more bytes; otherwise 4 waves x 4 steps, which keeps
   // more blocks resident per CU (measured best from 8 to 8192 rows).
   const long busy = (long)tiles * (long)std::min<long>(E, (long)T * k);
-#ifdef MM_MOE_FORCE
-  const int cfg = MM_MOE_FORCE;
-#else
   const int cfg = busy < 512 ? 0 : 1;
-#endif
 #define MM_LAUNCH_MOE(MTV, NWV, SPWV, FLV)                                                     \
   hipLaunchKernelGGL((k_moe_grouped<MTV, NWV, SPWV, FLV>), grid, dim3(NWV * 64), 0,               \
-                     (hipStream_t)stream, (const f16*)X, sorted_idx, offsets, gather, k, B,        \
-                     (const f16*)S, K, N, g, act, (f16*)Y)
+                     (hipStream_t)stream, (const f16*)X, sorted_idx, offsets, gather, k, W, K, N, g, \
+                     act, (f16*)Y)
 #define MM_LAUNCH_MOE_FL(MTV, NWV, SPWV)                                                       \
   switch (flush_steps(g, SPWV)) {                                                              \
     case 1: MM_LAUNCH_MOE(MTV, NWV, SPWV, 1); break;                                           \
@@ -516,45 +532,85 @@ extern "C" int mm_moe_grouped_gemm(const uint16_t* X, const int32_t* sorted_idx,
   return 0;
 }
 
-extern "C" int mm_moe_combine(const uint16_t* Y, const float* probs, const int32_t* inverse,
-                              int T, int k, int H, uint16_t* out, void* stream) {
+
+int combine(const uint16_t* Y, const float* probs, const int32_t* inverse, int T, int k, int kin,
+            float wsh, const uint16_t* base, int H, uint16_t* out, void* stream) {
   MM_CHECK_ARG(T >= 0 && k > 0 && H > 0, "mm_moe_combine: bad shape");
   MM_CHECK_ARG(H % 8 == 0, "mm_moe_combine: H=%d must be divisible by 8", H);
   if (T == 0) return 0;
   hipLaunchKernelGGL(k_moe_combine, dim3(T), dim3(256), 0, (hipStream_t)stream, (const f16*)Y,
-                     probs, inverse, k, H, (f16*)out);
+                     probs, inverse, k, kin, wsh, (const f16*)base, H, (f16*)out);
   MM_CHECK_LAUNCH("mm_moe_combine");
   return 0;
 }
 
-// Routed-expert SwiGLU MLP in one call: stable sort -> gate_up (token gather
-// + SwiGLU epilogue) -> down -> probability-weighted combine, four launches
-// on one stream with no host synchronisation.  (Deriving each expert's rows
-// from the ids inside the GEMM blocks instead of sorting was measured and
-// rejected: no faster at T=32 and 20% slower at T=128, since every block
-// then scans all T*k ids before its first load.)
+// Routed-expert SwiGLU MLP: stable sort -> gate_up (token gather + SwiGLU
+// epilogue) -> down -> probability-weighted combine, four launches on one
+// stream with no host synchronisation.  (Deriving each expert's rows from the
+// ids inside the GEMM blocks instead of sorting was measured and rejected: no
+// faster at T=32 and 20% slower at T=128, since every block then scans all
+// T*k ids before its first load.)
+// With a shared expert (Bsgu != null) it is one more group, E, that every
+// token visits with weight wsh: its rows share the two grouped launches with
+// the routed experts' rows, and the combine adds it as slot k.  k may then be
+// 0 (the shared expert alone).  base (may be null) is added in the combine.
 template <typename IdT>
-int moe_mlp(const uint16_t* X, const IdT* ids, const float* probs, int T, int k, int E, int H,
-            int I, const uint32_t* Bgu, const uint16_t* Sgu, const uint32_t* Bdn,
-            const uint16_t* Sdn, int g, uint16_t* act_buf, uint16_t* y_buf, int32_t* sort_buf,
-            uint16_t* out, void* stream) {
-  MM_CHECK_ARG(T >= 0 && k > 0 && E > 0 && H > 0 && I > 0, "mm_moe_mlp_fp4: bad shape");
+int moe_mlp(const char* who, const uint16_t* X, const IdT* ids, const float* probs, int T, int k,
+            int E, int H, int I, const uint32_t* Bgu, const uint16_t* Sgu, const uint32_t* Bdn,
+            const uint16_t* Sdn, const uint32_t* Bsgu, const uint16_t* Ssgu, const uint32_t* Bsdn,
+            const uint16_t* Ssdn, float wsh, const uint16_t* base, int g, uint16_t* act_buf,
+            uint16_t* y_buf, int32_t* sort_buf, uint16_t* out, void* stream) {
+  const bool sh = Bsgu != nullptr;
+  MM_CHECK_ARG(T >= 0 && (k > 0 || (sh && k == 0)) && E >= 0 && H > 0 && I > 0 &&
+                   (E > 0 || sh),
+               "%s: bad shape", who);
+  MM_CHECK_ARG(!sh || (Ssgu != nullptr && Bsdn != nullptr && Ssdn != nullptr),
+               "%s: the shared expert needs all four of its tensors", who);
   if (T == 0) return 0;
   MM_CHECK_ARG(act_buf != nullptr && y_buf != nullptr && sort_buf != nullptr && out != nullptr,
-               "mm_moe_mlp_fp4: scratch and output buffers are required");
-  const long tk = (long)T * k;
+               "%s: scratch and output buffers are required", who);
+  const int G = E + (sh ? 1 : 0), kt = k + (sh ? 1 : 0);
+  const long tk = (long)T * kt;
   int32_t* offsets = sort_buf;
-  int32_t* sorted_idx = sort_buf + E + 1;
+  int32_t* sorted_idx = sort_buf + G + 1;
   int32_t* inverse = sorted_idx + tk;
-  int rc = moe_sort("mm_moe_mlp_fp4", ids, T, k, E, offsets, sorted_idx, inverse, stream);
+  int rc = moe_sort(who, ids, T, k, G, offsets, sorted_idx, inverse, stream, sh);
   if (rc) return rc;
-  rc = mm_moe_grouped_gemm(X, sorted_idx, offsets, 1, k, T, Bgu, Sgu, E, H, 2 * I, g, 1, act_buf,
-                           stream);
+  const ExpertW wgu{Bgu, (const f16*)Sgu, Bsgu, (const f16*)Ssgu, E};
+  const ExpertW wdn{Bdn, (const f16*)Sdn, Bsdn, (const f16*)Ssdn, E};
+  rc = grouped_gemm(X, sorted_idx, offsets, 1, kt, T, wgu, G, H, 2 * I, g, 1, act_buf, stream);
   if (rc) return rc;
-  rc = mm_moe_grouped_gemm(act_buf, sorted_idx, offsets, 0, k, T, Bdn, Sdn, E, I, H, g, 0, y_buf,
-                           stream);
+  rc = grouped_gemm(act_buf, sorted_idx, offsets, 0, kt, T, wdn, G, I, H, g, 0, y_buf, stream);
   if (rc) return rc;
-  return mm_moe_combine(y_buf, probs, inverse, T, k, H, out, stream);
+  return combine(y_buf, probs, inverse, T, kt, k, wsh, base, H, out, stream);
+}
+
+}  // namespace
+
+// ===========================================================================
+// C ABI
+// ===========================================================================
+extern "C" int mm_moe_sort(const int32_t* expert_ids, int T, int k, int E, int32_t* offsets,
+                           int32_t* sorted_idx, int32_t* inverse, void* stream) {
+  return moe_sort("mm_moe_sort", expert_ids, T, k, E, offsets, sorted_idx, inverse, stream);
+}
+
+extern "C" int mm_moe_sort_i64(const int64_t* expert_ids, int T, int k, int E, int32_t* offsets,
+                               int32_t* sorted_idx, int32_t* inverse, void* stream) {
+  return moe_sort("mm_moe_sort_i64", expert_ids, T, k, E, offsets, sorted_idx, inverse, stream);
+}
+
+extern "C" int mm_moe_grouped_gemm(const uint16_t* X, const int32_t* sorted_idx,
+                                   const int32_t* offsets, int gather, int k, int T,
+                                   const uint32_t* B, const uint16_t* S, int E, int K, int N,
+                                   int g, int act, uint16_t* Y, void* stream) {
+  return grouped_gemm(X, sorted_idx, offsets, gather, k, T,
+                      ExpertW{B, (const f16*)S, nullptr, nullptr, E}, E, K, N, g, act, Y, stream);
+}
+
+extern "C" int mm_moe_combine(const uint16_t* Y, const float* probs, const int32_t* inverse,
+                              int T, int k, int H, uint16_t* out, void* stream) {
+  return combine(Y, probs, inverse, T, k, k, 0.0f, nullptr, H, out, stream);
 }
 
 extern "C" int mm_moe_mlp_fp4(const uint16_t* X, const void* expert_ids, int ids_i64,
@@ -562,9 +618,32 @@ extern "C" int mm_moe_mlp_fp4(const uint16_t* X, const void* expert_ids, int ids
                               const uint32_t* Bgu, const uint16_t* Sgu, const uint32_t* Bdn,
                               const uint16_t* Sdn, int g, uint16_t* act_buf, uint16_t* y_buf,
                               int32_t* sort_buf, uint16_t* out, void* stream) {
+  const char* who = "mm_moe_mlp_fp4";
   if (ids_i64)
-    return moe_mlp<int64_t>(X, (const int64_t*)expert_ids, probs, T, k, E, H, I, Bgu, Sgu, Bdn, Sdn,
-                            g, act_buf, y_buf, sort_buf, out, stream);
-  return moe_mlp<int32_t>(X, (const int32_t*)expert_ids, probs, T, k, E, H, I, Bgu, Sgu, Bdn, Sdn,
-                          g, act_buf, y_buf, sort_buf, out, stream);
+    return moe_mlp(who, X, (const int64_t*)expert_ids, probs, T, k, E, H, I, Bgu, Sgu, Bdn, Sdn,
+                   nullptr, nullptr, nullptr, nullptr, 0.0f, nullptr, g, act_buf, y_buf, sort_buf,
+                   out, stream);
+  return moe_mlp(who, X, (const int32_t*)expert_ids, probs, T, k, E, H, I, Bgu, Sgu, Bdn, Sdn,
+                 nullptr, nullptr, nullptr, nullptr, 0.0f, nullptr, g, act_buf, y_buf, sort_buf,
+                 out, stream);
+}
+
+extern "C" int mm_moe_mlp_shared_fp4(const uint16_t* X, const void* expert_ids, int ids_i64,
+                                     const float* probs, int T, int k, int E, int H, int I,
+                                     const uint32_t* Bgu, const uint16_t* Sgu,
+                                     const uint32_t* Bdn, const uint16_t* Sdn,
+                                     const uint32_t* Bsgu, const uint16_t* Ssgu,
+                                     const uint32_t* Bsdn, const uint16_t* Ssdn,
+                                     float shared_weight, const uint16_t* base, int g,
+                                     uint16_t* act_buf, uint16_t* y_buf, int32_t* sort_buf,
+                                     uint16_t* out, void* stream) {
+  const char* who = "mm_moe_mlp_shared_fp4";
+  MM_CHECK_ARG(Bsgu != nullptr, "%s: the shared expert's gate_up weights are required", who);
+  if (ids_i64 || k == 0)
+    return moe_mlp(who, X, (const int64_t*)expert_ids, probs, T, k, E, H, I, Bgu, Sgu, Bdn, Sdn,
+                   Bsgu, Ssgu, Bsdn, Ssdn, shared_weight, base, g, act_buf, y_buf, sort_buf, out,
+                   stream);
+  return moe_mlp(who, X, (const int32_t*)expert_ids, probs, T, k, E, H, I, Bgu, Sgu, Bdn, Sdn,
+                 Bsgu, Ssgu, Bsdn, Ssdn, shared_weight, base, g, act_buf, y_buf, sort_buf, out,
+                 stream);
 }

@@ -326,3 +326,279 @@ class MoEDispatcher(nn.Module):
         if batch is not None:
             return combined.view(batch, seq, -1)
         return combined
+
+
+# ---------------------------------------------------------------------------
+# Expert MLP entry points with the reference's names, and the shared expert.
+# ---------------------------------------------------------------------------
+def _marlin_words(packed: torch.Tensor, K: int, N: int, name: str) -> torch.Tensor:
+    """[K/8, N] words; a row-packed [N, K/8] tensor (what the reference's
+    torch path also accepts, moe_dispatch.py:1397-1406) is transposed."""
+    if tuple(packed.shape) == (K // 8, N):
+        return packed.contiguous()
+    if tuple(packed.shape) == (N, K // 8):
+        return packed.t().contiguous()
+    raise ValueError(f"{name} shape {tuple(packed.shape)} is neither ({K // 8}, {N}) nor "
+                     f"({N}, {K // 8})")
+
+
+def _moe_mlp_shared(hidden: torch.Tensor, routed, shared, expert_ids, expert_probs,
+                    shared_weight: float, base: torch.Tensor | None, group_size: int
+                    ) -> torch.Tensor:
+    """One mm_moe_mlp_shared_fp4 call.  routed: (gu, gus, dn, dns) stacked
+    [E, ...] or None; shared: (gu, gus, dn, dns) of one expert."""
+    sgu, sgus, sdn, sdns = shared
+    x = _half(hidden)
+    T, H = x.shape
+    if sgus.dim() != 2 or sgus.shape[1] % 2 != 0:
+        raise ValueError(f"shared gate_up scales must be [H/g, 2I], got {tuple(sgus.shape)}")
+    I = sgus.shape[1] // 2
+    if H % group_size or I % group_size:
+        raise ValueError(f"hidden ({H}) and intermediate ({I}) must be divisible by "
+                         f"group_size ({group_size})")
+    sgu = _marlin_words(sgu, H, 2 * I, "shared gate_up packed")
+    sdn = _marlin_words(sdn, I, H, "shared down packed")
+    if tuple(sgus.shape) != (H // group_size, 2 * I) or \
+            tuple(sdns.shape) != (I // group_size, H):
+        raise ValueError("shared expert scales must be [H/g, 2I] and [I/g, H]")
+    dev = _lib.require_device(x, sgu, sgus, sdn, sdns, expert_ids, expert_probs, base)
+    if routed is None:
+        k, E = 0, 0
+        gu = gus = dn = dns = ids = p = None
+        i64 = 1
+    else:
+        gu, gus, dn, dns = routed
+        E = gu.shape[0]
+        if tuple(gu.shape) != (E, H // 8, 2 * I) or tuple(dn.shape) != (E, I // 8, H):
+            raise ValueError(f"routed weights must be [E, {H // 8}, {2 * I}] and "
+                             f"[E, {I // 8}, {H}] (the shared expert's intermediate size)")
+        if tuple(gus.shape) != (E, H // group_size, 2 * I) or \
+                tuple(dns.shape) != (E, I // group_size, H):
+            raise ValueError("routed scales must be [E, H/g, 2I] and [E, I/g, H]")
+        if expert_ids.dim() != 2 or expert_ids.shape[0] != T:
+            raise ValueError(f"expert_ids must be [{T}, top_k], got {tuple(expert_ids.shape)}")
+        k = expert_ids.shape[1]
+        i64 = int(expert_ids.dtype == torch.int64)
+        ids = expert_ids.contiguous() if i64 else expert_ids.to(torch.int32).contiguous()
+        p = expert_probs.to(torch.float32).contiguous()
+        gu, dn = gu.contiguous(), dn.contiguous()
+        gus, dns = _half(gus), _half(dns)
+    kt = k + 1
+    b = None if base is None else _half(base.reshape(T, H))
+    act = torch.empty((T * kt, I), dtype=torch.float16, device=dev)
+    y = torch.empty((T * kt, H), dtype=torch.float16, device=dev)
+    sort_buf = torch.empty(E + 2 + 2 * T * kt, dtype=torch.int32, device=dev)
+    out = torch.empty((T, H), dtype=torch.float16, device=dev)
+    _lib.call("mm_moe_mlp_shared_fp4", _lib.ptr(x), _lib.ptr(ids), i64, _lib.ptr(p), T, k, E, H,
+              I, _lib.ptr(gu), _lib.ptr(gus), _lib.ptr(dn), _lib.ptr(dns), _lib.ptr(sgu),
+              _lib.ptr(_half(sgus)), _lib.ptr(sdn), _lib.ptr(_half(sdns)), float(shared_weight),
+              _lib.ptr(b), group_size, _lib.ptr(act), _lib.ptr(y), _lib.ptr(sort_buf),
+              _lib.ptr(out), _lib.stream_of(x))
+    return out
+
+
+def _flatten_hidden(hidden: torch.Tensor):
+    if hidden.dim() < 2:
+        raise ValueError(f"hidden_states must be [..., hidden], got {tuple(hidden.shape)}")
+    return hidden.reshape(-1, hidden.shape[-1]), hidden.shape
+
+
+def _fused_expert_mlp(x: torch.Tensor, gate_up_packed: torch.Tensor,
+                      gate_up_scales: torch.Tensor, down_packed: torch.Tensor,
+                      down_scales: torch.Tensor, group_size: int) -> torch.Tensor:
+    """One expert's SwiGLU MLP (moe_dispatch.py:1241-1431):
+    h = x @ W_gu ([H/8, 2I] packed; the row-packed [2I, H/8] is accepted too),
+    a = silu(h[:, :I]) * h[:, I:], y = a @ W_dn ([I/8, H]).  x [batch, H];
+    returns [batch, H] in x's dtype.  The gate_up product and the SwiGLU are
+    one launch, the down product a second (the sort is a trivial one-group
+    launch)."""
+    if x.dim() != 2:
+        raise ValueError(f"x must be [batch, hidden], got {tuple(x.shape)}")
+    out = _moe_mlp_shared(x, None, (gate_up_packed, gate_up_scales, down_packed, down_scales),
+                          None, None, 1.0, None, group_size)
+    return out if x.dtype == torch.float16 else out.to(x.dtype)
+
+
+def moe_shared_expert_fp4(hidden_states: torch.Tensor, gate_up_packed: torch.Tensor,
+                          gate_up_scales: torch.Tensor, down_packed: torch.Tensor,
+                          down_scales: torch.Tensor, group_size: int = 128,
+                          shared_prob: float = 1.0) -> torch.Tensor:
+    """shared_prob * SwiGLU-MLP(hidden) for a shared expert (kernels/moe.py:
+    442-582): gate_up [H/8, 2I], down [I/8, H].  fp16 [..., H]."""
+    x, shape = _flatten_hidden(hidden_states)
+    out = _moe_mlp_shared(x, None, (gate_up_packed, gate_up_scales, down_packed, down_scales),
+                          None, None, shared_prob, None, group_size)
+    return out.reshape(*shape[:-1], out.shape[-1])
+
+
+def moe_add_shared_expert_fp4(hidden_states: torch.Tensor, moe_output: torch.Tensor,
+                              shared_gate_up_packed: torch.Tensor,
+                              shared_gate_up_scales: torch.Tensor,
+                              shared_down_packed: torch.Tensor, shared_down_scales: torch.Tensor,
+                              group_size: int = 128) -> torch.Tensor:
+    """moe_output + SwiGLU-MLP_shared(hidden) (kernels/moe.py:858-930); the
+    addition happens in the combine launch, in fp32.  fp16 [..., H]."""
+    x, shape = _flatten_hidden(hidden_states)
+    if moe_output.shape != x.shape and moe_output.shape != shape:
+        raise ValueError(f"moe_output shape {tuple(moe_output.shape)} doesn't match hidden "
+                         f"shape {tuple(x.shape)}")
+    out = _moe_mlp_shared(x, None, (shared_gate_up_packed, shared_gate_up_scales,
+                                    shared_down_packed, shared_down_scales),
+                          None, None, 1.0, moe_output, group_size)
+    return out.reshape(*shape[:-1], out.shape[-1])
+
+
+def moe_fused_dispatch_shared_fp4(hidden_states: torch.Tensor,
+                                  shared_gate_up_packed: torch.Tensor,
+                                  shared_gate_up_scales: torch.Tensor,
+                                  shared_down_packed: torch.Tensor,
+                                  shared_down_scales: torch.Tensor,
+                                  routed_gate_up_packed: torch.Tensor,
+                                  routed_gate_up_scales: torch.Tensor,
+                                  routed_down_packed: torch.Tensor,
+                                  routed_down_scales: torch.Tensor,
+                                  expert_ids: torch.Tensor, expert_probs: torch.Tensor,
+                                  group_size: int = 128) -> torch.Tensor:
+    """Routed experts plus a shared expert (kernels/moe.py:742-856):
+    out[t] = MLP_shared(x[t]) + sum_j p[t, j] * MLP_{e(t, j)}(x[t]).
+    Shared weights [H/8, 2I] / [I/8, H], routed [E, H/8, 2I] / [E, I/8, H]
+    (same intermediate size, as the reference requires).  The shared expert is
+    one more group of the two grouped launches.  fp16 [..., H]."""
+    x, shape = _flatten_hidden(hidden_states)
+    H = x.shape[-1]
+    if H % 8 != 0:
+        raise ValueError(f"hidden_dim ({H}) must be divisible by 8")
+    if H % group_size != 0:
+        raise ValueError(f"hidden_dim ({H}) must be divisible by group_size ({group_size})")
+    out = _moe_mlp_shared(
+        x, (routed_gate_up_packed, routed_gate_up_scales, routed_down_packed, routed_down_scales),
+        (shared_gate_up_packed, shared_gate_up_scales, shared_down_packed, shared_down_scales),
+        expert_ids, expert_probs, 1.0, None, group_size)
+    return out.reshape(*shape[:-1], H)
+
+
+class FusedMoEDispatcher(nn.Module):
+    """MoE with a shared expert in one fused pass (moe_dispatch.py:1111-1238):
+    output = shared_expert(x) + sum_k prob[k] * routed_expert_k(x), with
+    softmax -> top-k (no renormalisation) routing of the given logits.
+    Weights: routed gate_up [E, H/8, 2I] (scales [E, H/g, 2I]), down
+    [E, I/8, H] (scales [E, I/g, H]); shared gate_up [H/8, 2I], down [I/8, H]."""
+
+    def __init__(self, num_experts: int, num_experts_per_tok: int,
+                 expert_gate_up_weights: torch.Tensor, expert_gate_up_scales: torch.Tensor,
+                 expert_down_weights: torch.Tensor, expert_down_scales: torch.Tensor,
+                 shared_gate_up_weights: torch.Tensor, shared_gate_up_scales: torch.Tensor,
+                 shared_down_weights: torch.Tensor, shared_down_scales: torch.Tensor,
+                 group_size: int = 128) -> None:
+        super().__init__()
+        self.num_experts = num_experts
+        self.num_experts_per_tok = num_experts_per_tok
+        self.group_size = group_size
+        self.register_buffer("expert_gate_up_weights", expert_gate_up_weights)
+        self.register_buffer("expert_gate_up_scales", expert_gate_up_scales)
+        self.register_buffer("expert_down_weights", expert_down_weights)
+        self.register_buffer("expert_down_scales", expert_down_scales)
+        self.register_buffer("shared_gate_up_weights", shared_gate_up_weights)
+        self.register_buffer("shared_gate_up_scales", shared_gate_up_scales)
+        self.register_buffer("shared_down_weights", shared_down_weights)
+        self.register_buffer("shared_down_scales", shared_down_scales)
+
+    def forward(self, hidden: torch.Tensor, gate_logits: torch.Tensor) -> torch.Tensor:
+        if hidden.dim() == 3:
+            batch, seq, hd = hidden.shape
+            flat = hidden.reshape(-1, hd)
+        else:
+            flat, batch, seq = hidden, None, None
+        if gate_logits.dim() != 2:
+            raise ValueError("gate_logits must be [tokens, num_experts]")
+        if gate_logits.shape[0] != flat.shape[0]:
+            raise ValueError("gate_logits batch must match hidden tokens")
+        probs, ids = _softmax_topk(gate_logits, self.num_experts_per_tok, False)
+        out = moe_fused_dispatch_shared_fp4(
+            flat, self.shared_gate_up_weights, self.shared_gate_up_scales,
+            self.shared_down_weights, self.shared_down_scales, self.expert_gate_up_weights,
+            self.expert_gate_up_scales, self.expert_down_weights, self.expert_down_scales,
+            ids, probs, self.group_size)
+        if batch is not None:
+            return out.view(batch, seq, -1)
+        return out
+
+
+def _expert_tensors(expert) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """One expert module's weights as Marlin-layout gate_up [H/8, 2I] with
+    scales [H/g, 2I] and down [I/8, H] with scales [I/g, H].  Experts hold
+    row-packed layers ([out, in/8] words, [n_groups, out] scales): either
+    gate_proj and up_proj (what moe_dispatch.py:2623-2636 stacks) or one fused
+    gate_up_proj (layers/mmfp4_expert.py:193-250)."""
+    if hasattr(expert, "gate_up_proj"):
+        gu_rows = expert.gate_up_proj.packed_weights
+        gu_s = expert.gate_up_proj.scales
+    else:
+        gu_rows = torch.cat([expert.gate_proj.packed_weights, expert.up_proj.packed_weights], 0)
+        gu_s = torch.cat([expert.gate_proj.scales, expert.up_proj.scales], 1)
+    dn = expert.down_proj
+    return (gu_rows.t().contiguous(), gu_s.to(torch.float16).contiguous(),
+            dn.packed_weights.t().contiguous(), dn.scales.to(torch.float16).contiguous())
+
+
+def _stacked_expert_weights(experts, n_experts: int):
+    """[E, ...] Marlin-layout stacks of every expert's weights, built once and
+    kept on the ModuleList until one of the source tensors is replaced or
+    written (keyed on data pointers and version counters)."""
+    srcs = []
+    for e in range(n_experts):
+        ex = experts[e]
+        layers = ([ex.gate_up_proj] if hasattr(ex, "gate_up_proj")
+                  else [ex.gate_proj, ex.up_proj]) + [ex.down_proj]
+        for lyr in layers:
+            for t in (lyr.packed_weights, lyr.scales):
+                srcs.append((t.data_ptr(), t._version))
+    key = tuple(srcs)
+    cached = getattr(experts, "_mmfp4_stacked", None)
+    if cached is not None and cached[0] == key:
+        return cached[1]
+    parts = [_expert_tensors(experts[e]) for e in range(n_experts)]
+    stacked = tuple(torch.stack([p[i] for p in parts], 0) for i in range(4))
+    experts._mmfp4_stacked = (key, stacked)
+    return stacked
+
+
+def dispatch_experts_batched(expert_inputs: torch.Tensor, experts, dispatch_info: MoEDispatchInfo,
+                             n_experts: int, batch_size: int = 16) -> torch.Tensor:
+    """Every expert's SwiGLU MLP over its rows of the expert-sorted inputs
+    (moe_dispatch.py:2546-2676): expert_inputs [T*k, H] in sorted order (the
+    output of gather_for_experts), rows offsets[e]..offsets[e+1] go to
+    experts[e].  Returns [T*k, H] in sorted order, expert_inputs' dtype.
+    The reference stacks weights per batch of `batch_size` experts and runs
+    one fused MLP per expert; here the stacked weights are cached and all
+    experts run in two grouped launches (gate_up + SwiGLU, down), so
+    `batch_size` has no effect."""
+    del batch_size
+    dev = _lib.require_device(expert_inputs)
+    total, H = expert_inputs.shape
+    out_dtype = expert_inputs.dtype
+    if total == 0:
+        return expert_inputs.new_empty((0, H))
+    gs = {int(experts[e].group_size) for e in range(n_experts)}
+    if len(gs) != 1:
+        raise ValueError(f"experts use different group sizes {sorted(gs)}")
+    g = gs.pop()
+    gu, gus, dn, dns = _stacked_expert_weights(experts, n_experts)
+    if gu.device != dev:
+        raise RuntimeError(f"expert weights on {gu.device}, inputs on {dev}")
+    E, HP, N2 = gu.shape
+    if HP * 8 != H:
+        raise ValueError(f"expert hidden size {HP * 8} != inputs' {H}")
+    I = N2 // 2
+    offs = dispatch_info.expert_offsets.to(device=dev, dtype=torch.int32).contiguous()
+    if offs.numel() != n_experts + 1:
+        raise ValueError(f"dispatch_info has {offs.numel() - 1} experts, expected {n_experts}")
+    x = _half(expert_inputs)
+    act = torch.empty((total, I), dtype=torch.float16, device=dev)
+    y = torch.empty((total, H), dtype=torch.float16, device=dev)
+    st = _lib.stream_of(x)
+    _lib.call("mm_moe_grouped_gemm", _lib.ptr(x), None, _lib.ptr(offs), 0, 1, total,
+              _lib.ptr(gu), _lib.ptr(gus), E, H, N2, g, 1, _lib.ptr(act), st)
+    _lib.call("mm_moe_grouped_gemm", _lib.ptr(act), None, _lib.ptr(offs), 0, 1, total,
+              _lib.ptr(dn), _lib.ptr(dns), E, I, H, g, 0, _lib.ptr(y), st)
+    return y if out_dtype == torch.float16 else y.to(out_dtype)

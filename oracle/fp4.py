@@ -224,7 +224,9 @@ def flat_dequantize(codes: np.ndarray, scales: np.ndarray, group_size: int = 128
     n = flat.shape[0]
     padded = np.zeros(s.shape[0] * group_size, np.float32)
     padded[:n] = flat
-    return (padded.reshape(-1, group_size) * s[:, None]).reshape(-1)[:n].reshape(c.shape)
+    with np.errstate(invalid="ignore"):
+        deq = padded.reshape(-1, group_size) * s[:, None]
+    return deq.reshape(-1)[:n].reshape(c.shape)
 
 
 def pack_pair(lo: np.ndarray, hi: np.ndarray) -> np.ndarray:
