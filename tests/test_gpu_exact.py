@@ -1,0 +1,177 @@
+"""Bit-exact GEMM parity on exact-arithmetic inputs, for every kernel family.
+
+Activations are small integers, weights are E2M1 codes (INT4: nibbles with
+integral zero points) times power-of-two group scales in [2^-4, 2^-1].
+Every product and every partial sum is then a multiple of 2^-5 (INT4: 2^-4)
+below 2^19, exactly representable in fp32 (as is the decode kernels' INT4
+form, integer sums of a * (1024 + q) below 2^19 per group), so the kernel's fp32 sums and the oracle's numpy
+fp32 matmul (tests/test_gemm.py:260-263's dequant + matmul) are the same
+exact value whatever the summation order, and one fp16 rounding gives the
+same bits.  A single dropped, duplicated or mis-indexed k row, column, group
+scale or split-K partial changes the output, which the max-abs-rel 1e-2 bar
+of the other parity tests cannot see.
+
+Each case is chosen to land on one kernel family (the selection rules of
+gemm_dispatch / pair_dispatch / mm_moe_grouped_gemm):
+  k_skinny_dual  M <= 8 narrow layers;  k_strip  8 < M <= 16, K*N <= 4096^2;
+  k_skinny       M <= 16 wide (no split) and split-K (14336 -> 4096), MT=2 for
+                 17..32 rows;  k_prefill2 M > 32 with K % 64 == 0 (and its
+                 split-K reduce when the grid is small);  k_prefill  N % 8 != 0
+                 or K % 64 != 0;  row-packed and [N, K/g]-scale variants;
+                 multi (QKV); gate/up pair (act=0, no SwiGLU rounding);
+                 k_moe_grouped and k_moe_prefill.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_helpers import announce, to_dev, to_np
+from oracle import fp4 as ofp4
+
+pytestmark = pytest.mark.gpu
+
+
+def _exact_fp4(rng, K, N, g):
+    """Random E2M1 codes and power-of-two scales in [2^-4, 2^-1] -> (packed [K/8, N], scales)."""
+    codes = rng.integers(0, 16, (K, N)).astype(np.uint8)
+    scales = (2.0 ** rng.integers(-4, 0, (K // g, N))).astype(np.float16)
+    return ofp4.pack_nibbles(codes), scales
+
+
+def _exact_u4(rng, K, N, g):
+    q = rng.integers(0, 16, (K, N)).astype(np.uint8)
+    scales = (2.0 ** rng.integers(-4, 0, (K // g, N))).astype(np.float16)
+    zeros = rng.integers(0, 16, (K // g, N)).astype(np.float16)
+    return ofp4.pack_nibbles(q), scales, zeros
+
+
+def _acts(rng, M, K):
+    return rng.integers(-3, 4, (M, K)).astype(np.float16)
+
+
+def _bits(x) -> np.ndarray:
+    return np.asarray(x, np.float16).view(np.uint16)
+
+
+def _same(out: torch.Tensor, ref: np.ndarray):
+    o = to_np(out)
+    assert o.shape == ref.shape
+    bad = np.nonzero(_bits(o) != _bits(ref))
+    assert bad[0].size == 0, (f"{bad[0].size} outputs differ, first at {bad[0][0]},{bad[1][0]}: "
+                              f"{o[bad[0][0], bad[1][0]]} vs {ref[bad[0][0], bad[1][0]]}")
+
+
+DENSE = [
+    # (M, K, N, g, family)
+    (1, 4096, 6144, 128, "k_skinny_dual (qkv)"),
+    (8, 4096, 4096, 128, "k_skinny_dual (small layer)"),
+    (5, 4160, 3076, 64, "k_skinny_dual ragged"),
+    (12, 4096, 4096, 128, "k_strip"),
+    (16, 2048, 2048, 32, "k_strip g=32"),
+    (1, 4096, 28672, 128, "k_skinny unsplit"),
+    (1, 14336, 4096, 128, "k_skinny split-K"),
+    (13, 14336, 4096, 64, "k_skinny split-K M=13"),
+    (24, 4096, 28672, 128, "k_skinny MT=2"),
+    (32, 14336, 4096, 128, "k_skinny MT=2 split-K"),
+    (64, 4096, 1024, 128, "k_prefill2 64-row tile"),
+    (128, 14336, 4096, 128, "k_prefill2 split-K + reduce"),
+    (512, 4096, 14336, 128, "k_prefill2 (cfg4 M=512)"),
+    (300, 2048, 1000, 64, "k_prefill2 ragged"),
+    (100, 520, 260, 8, "k_prefill (N % 8, K % 64)"),
+    (40, 200, 96, 8, "k_prefill (K % 64)"),
+]
+
+
+@pytest.mark.parametrize("M,K,N,g,family", DENSE)
+def test_fp4_gemm_bit_exact(rng, M, K, N, g, family):
+    import mmfp4
+    packed, scales = _exact_fp4(rng, K, N, g)
+    a = _acts(rng, M, K)
+    ref = ofp4.gemm_fp4_ref(a, packed, scales, g)
+    announce(f"exact fp4 {family} M={M} K={K} N={N} g={g}")
+    _same(mmfp4.marlin_gemm_fp4(to_dev(a), to_dev(packed), to_dev(scales), g), ref)
+
+
+@pytest.mark.parametrize("M,K,N,g,family", [d for d in DENSE if d[0] in (1, 12, 13, 24, 64, 128,
+                                                                          100)])
+def test_u4_gemm_bit_exact(rng, M, K, N, g, family):
+    import mmfp4
+    packed, s, z = _exact_u4(rng, K, N, g)
+    a = _acts(rng, M, K)
+    ref = ofp4.gemm_u4_ref(a, packed, s, z, g)
+    announce(f"exact u4 {family} M={M} K={K} N={N} g={g}")
+    _same(mmfp4.marlin_gemm_int4(to_dev(a), to_dev(packed), to_dev(s), to_dev(z), g), ref)
+
+
+@pytest.mark.parametrize("M,K,N,g", [(1, 4096, 6144, 128), (1, 14336, 4096, 128),
+                                     (12, 4096, 4096, 64), (4, 4096, 28672, 128)])
+def test_rowpacked_and_mmfp4_bit_exact(rng, M, K, N, g):
+    """Row-packed words (both scale layouts) and Marlin words with [N, K/g]
+    scales: the two-slab and skinny in-place variants."""
+    import mmfp4
+    packed, scales = _exact_fp4(rng, K, N, g)
+    a = _acts(rng, M, K)
+    ref = ofp4.gemm_fp4_ref(a, packed, scales, g)
+    da = to_dev(a)
+    rows = to_dev(np.ascontiguousarray(packed.T))
+    announce(f"exact row-packed / mmfp4 M={M} K={K} N={N} g={g}")
+    _same(mmfp4.mmfp4_gemm_rowpacked(da, rows, to_dev(scales), g), ref)
+    _same(mmfp4.mmfp4_gemm_rowpacked(da, rows, to_dev(np.ascontiguousarray(scales.T)), g), ref)
+    _same(mmfp4.mmfp4_gemm(da, to_dev(packed), to_dev(np.ascontiguousarray(scales.T)), g), ref)
+
+
+@pytest.mark.parametrize("M", [1, 12, 48])
+def test_multi_qkv_bit_exact(rng, M):
+    import mmfp4
+    K, g = 4096, 128
+    mats = [_exact_fp4(rng, K, n, g) for n in (4096, 1024, 1024)]
+    a = _acts(rng, M, K)
+    announce(f"exact qkv M={M}")
+    outs = mmfp4.mmfp4_fused_qkv(to_dev(a), *[to_dev(t) for m in mats for t in m], g)
+    for o, (p, s) in zip(outs, mats):
+        _same(o, ofp4.gemm_fp4_ref(a, p, s, g))
+
+
+@pytest.mark.parametrize("M", [1, 24, 256])
+def test_gate_up_pair_bit_exact(rng, M):
+    """Pair mode without the SwiGLU (act=0): [x @ Wg | x @ Wu]."""
+    import mmfp4
+    K, N, g = 4096, 3072, 128
+    gp, gs = _exact_fp4(rng, K, N, g)
+    up, us = _exact_fp4(rng, K, N, g)
+    a = _acts(rng, M, K)
+    ref = np.concatenate([ofp4.gemm_fp4_ref(a, gp, gs, g), ofp4.gemm_fp4_ref(a, up, us, g)], 1)
+    announce(f"exact gate/up pair M={M}")
+    _same(mmfp4.fused_gate_up_gemm(to_dev(a), to_dev(gp), to_dev(gs), to_dev(up), to_dev(us), g),
+          ref)
+
+
+@pytest.mark.parametrize("T,k,E,K,N", [(32, 8, 128, 2048, 1536), (32, 8, 128, 768, 2048),
+                                       (1024, 8, 128, 2048, 1536), (1024, 8, 128, 768, 2048),
+                                       (7, 3, 5, 256, 96)])
+def test_grouped_gemm_bit_exact(rng, T, k, E, K, N):
+    """Grouped expert GEMM rows (gathered, no activation) at the config-5
+    shapes: decode-sized groups (k_moe_grouped) at T=32, prefill-sized
+    (k_moe_prefill) at T=1024.  Row r of expert e is fp16(x[token(r)] @ W_e)."""
+    import mmfp4
+    from mmfp4 import moe_dispatch as md
+    g = 128
+    parts = [_exact_fp4(rng, K, N, g) for _ in range(E)]
+    P = np.stack([p for p, _ in parts])
+    S = np.stack([s for _, s in parts])
+    x = _acts(rng, T, K)
+    ids = np.stack([rng.permutation(E)[:k] for _ in range(T)]).astype(np.int32)
+    sidx, offs, _ = md._sort(to_dev(ids), E)
+    announce(f"exact grouped T={T} k={k} E={E} K={K} N={N}")
+    y = md._grouped(to_dev(x), sidx, offs, True, k, T, to_dev(P), to_dev(S), g, 0)
+    s_np = to_np(sidx).astype(np.int64)
+    o_np = to_np(offs)
+    ref = np.empty((T * k, N), np.float16)
+    for e in range(E):
+        r0, r1 = o_np[e], o_np[e + 1]
+        if r1 > r0:
+            ref[r0:r1] = ofp4.gemm_fp4_ref(x[s_np[r0:r1] // k], P[e], S[e], g)
+    _same(y, ref)

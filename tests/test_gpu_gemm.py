@@ -89,7 +89,7 @@ def test_fp4_decode_llama_layers(M, K, N):
     assert max_abs_rel(to_np(out), to_np(ref)) <= TOL
 
 
-@pytest.mark.parametrize("M", [512, 2048])
+@pytest.mark.parametrize("M", [512, 2048, 8192])
 @pytest.mark.parametrize("K,N", [(4096, 14336), (14336, 4096)])
 def test_fp4_prefill_config4(M, K, N):
     import mmfp4
@@ -111,6 +111,33 @@ def test_u4_llama_layers(M, K, N):
     announce(f"u4 layer M={M} K={K} N={N}")
     out = mmfp4.marlin_gemm_int4(a, packed, s, z, 128)
     assert max_abs_rel(to_np(out), to_np(ref)) <= TOL
+
+
+@pytest.mark.parametrize("M", [1, 16, 64])
+def test_u4_outlier_activations(rng, M):
+    """INT4 with LLM-like activations: a few channels at +-100 .. +-1000 over an
+    N(0, 1) body.  The decode kernels sum a * (1024 + q) and subtract
+    (1024 + z) * sum(a) per group, a cancellation whose rounding grows with
+    1024 * sum|a|; the prefill kernel uses the dequantized weights.  Against
+    the oracle's fp32 (q - z) * s matmul."""
+    import mmfp4
+    K, N, g = 4096, 1024, 128
+    w = rng.normal(0, 0.02, (N, K)).astype(np.float16)
+    packed, s, z = ofp4.pack_u4_weights(w, g)
+    a = rng.normal(0, 1, (M, K)).astype(np.float32)
+    chans = rng.choice(K, 24, replace=False)
+    a[:, chans] = rng.choice([-1000.0, -300.0, -100.0, 100.0, 250.0, 1000.0], (M, 24))
+    a = a.astype(np.float16)
+    ref = ofp4.gemm_u4_ref(a, packed, s, z, g)
+    announce(f"u4 outliers M={M}")
+    out = to_np(mmfp4.marlin_gemm_int4(to_dev(a), to_dev(packed), to_dev(s), to_dev(z), g))
+    assert max_abs_rel(out, ref) <= TOL
+    # the body columns alone (outlier contributions removed) are still matched
+    a2 = a.copy()
+    a2[:, chans] = 0
+    body = ofp4.gemm_u4_ref(a2, packed, s, z, g)
+    out2 = to_np(mmfp4.marlin_gemm_int4(to_dev(a2), to_dev(packed), to_dev(s), to_dev(z), g))
+    assert max_abs_rel(out2, body) <= TOL
 
 
 @pytest.mark.parametrize("M", [1, 20, 64])

@@ -152,6 +152,36 @@ def test_moe_prefill_config5_properties():
     assert max_abs_rel(to_np(out), to_np(ref)) <= TOL
 
 
+def test_moe_prefill_config5_vs_oracle_subset():
+    """Config 5 at T=1024 (Qwen3-30B-A3B: E=128, H=2048, I=768, top-8) against
+    the oracle's per-token fp32 brute force on a seeded subset of 24 tokens
+    (each token's output depends only on its own routing, so the subset is
+    exact).  Weights come from the GPU quantizer, which is bit-exact with the
+    oracle's (test_gpu_dequant_quant.py)."""
+    import mmfp4
+    E, T, k, H, I, g = 128, 1024, 8, 2048, 768, 128
+    gen = torch.Generator(device="cuda").manual_seed(12)
+    GU = torch.empty((E, H // 8, 2 * I), dtype=torch.int32, device="cuda")
+    GS = torch.empty((E, H // g, 2 * I), dtype=torch.float16, device="cuda")
+    DP = torch.empty((E, I // 8, H), dtype=torch.int32, device="cuda")
+    DS = torch.empty((E, I // g, H), dtype=torch.float16, device="cuda")
+    for e in range(E):
+        w1 = (torch.randn((2 * I, H), generator=gen, device="cuda") * 0.02).half()
+        w2 = (torch.randn((H, I), generator=gen, device="cuda") * 0.02).half()
+        GU[e], GS[e] = mmfp4.quantize_fp4(w1, group_size=g)
+        DP[e], DS[e] = mmfp4.quantize_fp4(w2, group_size=g)
+    x = torch.randn((T, H), generator=gen, device="cuda").half()
+    logits = torch.randn((T, E), generator=gen, device="cuda")
+    probs, ids = mmfp4.router_softmax_topk(logits, k)
+    announce("moe prefill T=1024 vs oracle subset")
+    out = to_np(mmfp4.moe_mlp_fp4(x, GU, GS, DP, DS, ids, probs, g))
+    sub = np.random.default_rng(5).choice(T, 24, replace=False)
+    ids_s = to_np(ids)[sub]
+    ref = omoe.moe_forward_ref(to_np(x)[sub], to_np(GU).view(np.uint32), to_np(GS),
+                               to_np(DP).view(np.uint32), to_np(DS), ids_s, to_np(probs)[sub], g)
+    assert max_abs_rel(out[sub], ref) <= TOL
+
+
 @pytest.mark.parametrize("T,k,E", [(5, 2, 4), (256, 8, 128), (1, 4, 64)])
 def test_gpu_grouping_api(rng, T, k, E):
     """moe/gpu_grouping.py surface: every variant gives the oracle's stable order;
@@ -212,9 +242,9 @@ def test_moe_mlp_one_call_matches_steps(rng, E, T, k, H, I, i64):
 
 
 def test_moe_mlp_back_to_back_calls(rng):
-    """Decode-sized calls form the output in the down launch (last block per
-    128 columns, arrival counters cleared by the sort): consecutive calls of
-    different sizes on one stream each match their step-by-step result."""
+    """Consecutive decode-sized calls of different sizes on one stream (the
+    sort, grouped GEMMs and combine reuse nothing between calls) each match
+    their step-by-step result."""
     import mmfp4
     from mmfp4 import moe_dispatch as md
     E, H, I, k, g = 32, 512, 256, 4, 128
