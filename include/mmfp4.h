@@ -85,6 +85,18 @@ int mm_fp4_gemm_rowpacked(const uint16_t* A, const uint32_t* B, const uint16_t* 
                           uint16_t* C, int M, int N, int K, int group_size, int scales_layout,
                           void* ws, size_t ws_bytes, void* stream);
 
+/* mm_fp4_gemm without a workspace argument, for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference.  The split-K counters and
+ * partial sums live in a 32 MiB device array built into the library (one copy
+ * per device, held until the process ends); a shape whose
+ * mm_gemm_workspace_bytes(M, N, K) exceeds 32 MiB is refused (status 1).  The
+ * call makes no allocation.  All calls on one device share that device's
+ * array, so calls that overlap on a device (several streams or threads) race.
+ * Otherwise as mm_fp4_gemm, with the same results. */
+int mm_fp4_gemm_noalloc(const uint16_t* A, const uint32_t* B, const uint16_t* scales, uint16_t* C,
+                        int M, int N, int K, int group_size, void* stream);
+
 /* INT4 asymmetric counterpart.  Replaces metal_marlin/kernels_core.py:1959-2066
  * (marlin_gemm_int4) and metal_marlin/metal_dispatch.py:1863-1937
  * (MetalKernelLibrary.int4_gemm). */

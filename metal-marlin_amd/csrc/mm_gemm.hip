@@ -15,6 +15,7 @@
 //    (deterministic order, counter left at zero for the next call).
 //  * prefill (M > 32): 32x32x16 MFMA tiles, A double-buffered through LDS,
 //    B loaded as packed words one chunk ahead and dequantised in registers.
+#include <mutex>
 #include <type_traits>
 
 #include "mm_common.h"
@@ -1189,4 +1190,72 @@ extern "C" int mm_fp4_gemm_multi(const uint16_t* A, int nmat, const uint32_t* co
                                  int K, int g, void* ws, size_t ws_bytes, void* stream) {
   return multi_dispatch("mm_fp4_gemm_multi", (const f16*)A, nmat, B, (const f16* const*)S,
                         (f16* const*)C, N, M, K, g, ws, ws_bytes, (hipStream_t)stream);
+}
+
+// ===========================================================================
+// No-allocation variant of mm_fp4_gemm: the workspace (split-K arrival
+// counters and partial sums) is a file-scope device array, so a call makes no
+// allocation of any kind.  Each device holds its own copy of the array for the
+// life of the process; its address on a device is looked up once, with that
+// device current, and kept per device.  The kernels leave the counters at zero
+// after every call, so the array needs clearing only once (at set-up).  Every
+// call on a device shares that device's array: calls that overlap on one
+// device (several streams or threads) race.
+// ===========================================================================
+namespace {
+
+constexpr size_t MM_NOALLOC_SCRATCH_BYTES = (size_t)32 << 20;   // 32 MiB
+constexpr int MM_MAX_DEVICES = 64;
+
+__device__ __align__(256) uint8_t scratch[MM_NOALLOC_SCRATCH_BYTES];
+
+__global__ void __launch_bounds__(256) k_zero_words(uint32_t* p, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
+    p[i] = 0u;
+}
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[MM_MAX_DEVICES] = {};
+
+// Address of this device's scratch array (set up on first use).
+int noalloc_scratch(const char* who, hipStream_t st, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  MM_CHECK_ARG(e == hipSuccess && dev >= 0 && dev < MM_MAX_DEVICES,
+               "%s: no current HIP device (%s)", who, hipGetErrorString(e));
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    MM_CHECK_ARG(e == hipSuccess && p != nullptr,
+                 "%s: hipGetSymbolAddress(scratch) failed on device %d: %s", who, dev,
+                 hipGetErrorString(e));
+    // Clear the counter block once (a fill kernel: no memset node for a
+    // caller that captures this stream).
+    hipLaunchKernelGGL(k_zero_words, dim3(64), dim3(256), 0, st, (uint32_t*)p,
+                       SK_COUNTER_BYTES / sizeof(uint32_t));
+    MM_CHECK_LAUNCH(who);
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+
+}  // namespace
+
+extern "C" int mm_fp4_gemm_noalloc(const uint16_t* A, const uint32_t* B, const uint16_t* S,
+                                   uint16_t* C, int M, int N, int K, int g, void* stream) {
+  const char* who = "mm_fp4_gemm_noalloc";
+  MM_CHECK_ARG(M >= 0 && N > 0 && K > 0, "%s: bad shape M=%d N=%d K=%d", who, M, N, K);
+  const size_t need = mm_gemm_workspace_bytes(M, N, K);
+  MM_CHECK_ARG(need <= MM_NOALLOC_SCRATCH_BYTES,
+               "%s: M=%d N=%d K=%d needs %zu bytes of workspace, more than the %zu-byte "
+               "built-in scratch (call mm_fp4_gemm with a workspace instead)",
+               who, M, N, K, need, MM_NOALLOC_SCRATCH_BYTES);
+  hipStream_t st = (hipStream_t)stream;
+  void* ws = nullptr;
+  const int rc = noalloc_scratch(who, st, &ws);
+  if (rc) return rc;
+  return gemm_dispatch<false>(who, (const f16*)A, B, (const f16*)S, nullptr, (f16*)C, M, N, K, g,
+                              ws, MM_NOALLOC_SCRATCH_BYTES, st);
 }

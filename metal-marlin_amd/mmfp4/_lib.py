@@ -27,6 +27,7 @@ SIGNATURES: dict[str, tuple] = {
     "mm_gemm_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int]),
     "mm_fp4_gemm": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _c_size,
                              _vp]),
+    "mm_fp4_gemm_noalloc": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp]),
     "mm_fp4_gemm_rowpacked": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int,
                                        _c_int, _vp, _c_size, _vp]),
     "mm_fp4_gemm_mmfp4": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp,
