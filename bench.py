@@ -222,6 +222,60 @@ def rand_weights(torch, K: int, N: int, gen):
     return p, s
 
 
+def run_north_star_decode(torch, mmfp4, steps: int):
+    """The north star's decode shapes at M=1 (4096 -> 14336 and 14336 -> 4096),
+    each on its own with rotated weight copies: µs per launch, algorithmic
+    TB/s, fraction of HBM peak and of the 0.70 target."""
+    out = {}
+    for name, K, N in (("4096x14336", 4096, 14336), ("14336x4096", 14336, 4096)):
+        copies = max(2, -(-ROTATE_BYTES // alg_bytes(0, K, N)))
+        ws = [make_weights(torch, mmfp4, K, N, 700 + c) for c in range(copies)]
+        a = torch.randn((1, K), device="cuda").half()
+        launches = [[lambda w=w: mmfp4.marlin_gemm_fp4(a, w[0], w[1], G)] for w in ws]
+        us = 1e3 * timed_launches(torch, launches, steps, 10) / steps
+        tbs = alg_bytes(1, K, N) / (us * 1e-6) / 1e12
+        out[name] = {"us": round(us, 3), "TBps": round(tbs, 3),
+                     "frac_hbm_peak": round(tbs * 1e3 / HBM_PEAK_GBS, 4),
+                     "frac_of_0.70_target": round(tbs * 1e3 / HBM_PEAK_GBS / 0.70, 4)}
+        del ws
+    return out
+
+
+def run_host_paced(torch, mmfp4, n: int = 400):
+    """Per-call latency as a caller without a captured graph sees it: the
+    Python-level enqueue time per marlin_gemm_fp4 call, and the wall time per
+    call of back-to-back calls synchronised once at the end (no GPU-side
+    queue-ahead)."""
+    out = {}
+    for name, M, K, N in (("config1_4096x4096_M1", 1, 4096, 4096),
+                          ("4096x14336_M1", 1, 4096, 14336)):
+        w = make_weights(torch, mmfp4, K, N, 800)
+        a = torch.randn((M, K), device="cuda").half()
+        for _ in range(20):
+            mmfp4.marlin_gemm_fp4(a, w[0], w[1], G)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            mmfp4.marlin_gemm_fp4(a, w[0], w[1], G)
+        t1 = time.perf_counter()
+        torch.cuda.synchronize()
+        t2 = time.perf_counter()
+        out[name] = {"host_enqueue_us_per_call": round(1e6 * (t1 - t0) / n, 2),
+                     "wall_us_per_call": round(1e6 * (t2 - t0) / n, 2)}
+    return out
+
+
+def cpu_model_name() -> str:
+    """The host CPU's model name (what lscpu prints), from /proc/cpuinfo."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.lower().startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
 def run_fused_bench(torch, mmfp4, steps: int):
     """The operators either side of the GEMM at the Llama-3-8B and Qwen3 MoE
     shapes, fused vs unfused, rotated weight copies: gate_up+SiLU (4096 ->
@@ -407,8 +461,9 @@ def cpu_baseline(budget_s: float = 15.0):
     step_bytes = sum(alg_bytes(1, K, N) for _, K, N in LLAMA_LAYER)
     return {"value": round(step_bytes / dt / 1e12, 6), "unit": "TB/s", "cores": cores,
             "kind": "port", "ms_per_step": round(dt * 1e3, 1),
+            "cpu_model": cpu_model_name(),
             "sample": f"{steps} step(s) of the 4-GEMM Llama-3-8B layer at M=1 "
-                      f"(torch-CPU fp32 dequant+matmul, {platform.processor() or 'host'})"}
+                      f"(torch-CPU fp32 dequant+matmul)"}
 
 
 def pmc_probe(torch, mmfp4) -> int:
@@ -539,6 +594,8 @@ def main() -> int:
     ceil["layer_time_fraction"] = round(ceil["layer_us"] / (1e3 * layer["ms_per_step"]), 4)
     out["hbm_read_ceiling_m1"] = ceil
     out["config1_single_linear_m1"] = run_single_bench(torch, mmfp4, 1, 4096, 4096, 100)
+    out["north_star_decode_m1"] = run_north_star_decode(torch, mmfp4, 100)
+    out["host_paced_per_call"] = run_host_paced(torch, mmfp4)
     out["config5_moe_qwen3_30b_a3b"] = [run_moe_bench(torch, mmfp4, T, 20) for T in (32, 1024)]
     out["prefill_m2048"]["hipblaslt_fp16_same_shapes"] = hipblaslt_fp16_reference(torch, 2048)
     out["prefill_m2048"]["mfma_ceiling"] = run_mfma_ceiling(torch, mmfp4, tflops)

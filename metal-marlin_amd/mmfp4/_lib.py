@@ -65,8 +65,33 @@ _lib = None
 _lock = threading.Lock()
 
 
+class _Bound:
+    """The entry points as attributes, bound once at load (no per-call
+    getattr on the CDLL)."""
+
+
+F = _Bound()
+
+
 class MMError(RuntimeError):
     """A libmmfp4 entry point returned a non-zero status."""
+
+
+_binding = None
+
+
+def binding():
+    """The per-call torch binding (_mmfp4_torch.so, built next to the library)
+    or None when it was not built; both call the same C ABI."""
+    global _binding
+    if _binding is None:
+        load()
+        try:
+            from . import _mmfp4_torch as b        # links libmmfp4.so from this directory
+        except ImportError:
+            b = False
+        _binding = b
+    return _binding or None
 
 
 def load() -> ctypes.CDLL:
@@ -85,27 +110,46 @@ def load() -> ctypes.CDLL:
                 fn = getattr(lib, name)
                 fn.restype = res
                 fn.argtypes = args
+                setattr(F, name, fn)
             _lib = lib
     return _lib
 
 
-def call(name: str, *args) -> None:
-    """Invoke entry point `name`; raise MMError (ValueError for bad arguments)."""
-    lib = load()
-    rc = getattr(lib, name)(*args)
+def check(rc: int) -> None:
+    """Raise for a non-zero status: ValueError for a bad argument (1),
+    MMError for a launch failure."""
     if rc != 0:
-        msg = lib.mm_last_error().decode(errors="replace")
+        msg = _lib.mm_last_error().decode(errors="replace")
         if rc == 1:
             raise ValueError(msg)
         raise MMError(msg)
+
+
+def call(name: str, *args) -> None:
+    """Invoke entry point `name`; raise MMError (ValueError for bad arguments)."""
+    if _lib is None:
+        load()
+    check(getattr(F, name)(*args))
 
 
 def ptr(t: torch.Tensor | None) -> ctypes.c_void_p:
     return ctypes.c_void_p(0 if t is None else t.data_ptr())
 
 
+try:                                   # current stream without a Stream object
+    _raw_stream = torch._C._cuda_getCurrentRawStream
+except AttributeError:                 # pragma: no cover - older torch
+    def _raw_stream(index: int) -> int:
+        return torch.cuda.current_stream(index).cuda_stream
+
+
+def raw_stream(device_index: int) -> int:
+    """Handle of the current torch stream on a device, as an integer."""
+    return _raw_stream(device_index)
+
+
 def stream_of(t: torch.Tensor) -> ctypes.c_void_p:
-    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+    return ctypes.c_void_p(_raw_stream(t.get_device()))
 
 
 def require_device(*tensors: torch.Tensor) -> torch.device:
@@ -116,7 +160,7 @@ def require_device(*tensors: torch.Tensor) -> torch.device:
             continue
         if not isinstance(t, torch.Tensor):
             raise TypeError(f"expected torch.Tensor, got {type(t).__name__}")
-        if t.device.type != "cuda":
+        if not t.is_cuda:
             raise RuntimeError(
                 f"tensor on {t.device}: the FP4/INT4 kernels run on the GPU only "
                 "(move inputs to a ROCm device)")
@@ -127,6 +171,25 @@ def require_device(*tensors: torch.Tensor) -> torch.device:
     return dev
 
 
+def same_device_index(*tensors: torch.Tensor) -> int:
+    """Device index shared by every (non-None) tensor, which must all be on a
+    ROCm device: the cheap check of the per-call hot path."""
+    idx = -1
+    for t in tensors:
+        if t is None:
+            continue
+        i = t.get_device()
+        if i < 0:
+            raise RuntimeError(
+                f"tensor on {t.device}: the FP4/INT4 kernels run on the GPU only "
+                "(move inputs to a ROCm device)")
+        if idx < 0:
+            idx = i
+        elif i != idx:
+            raise RuntimeError(f"tensors on different devices: cuda:{idx} vs cuda:{i}")
+    return idx
+
+
 # ---------------------------------------------------------------------------
 # Per-(device, stream) workspace.  Its head holds split-K arrival counters that
 # the kernels leave at zero, so it is allocated zeroed once and reused.
@@ -134,14 +197,19 @@ def require_device(*tensors: torch.Tensor) -> torch.device:
 _ws: dict[tuple[int, int], torch.Tensor] = {}
 
 
-def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    key = (device.index if device.index is not None else torch.cuda.current_device(),
-           torch.cuda.current_stream(device).cuda_stream)
+def workspace_on(index: int, stream: int, nbytes: int) -> torch.Tensor:
+    """Workspace of at least `nbytes` for (device index, raw stream)."""
+    key = (index, stream)
     buf = _ws.get(key)
     if buf is None or buf.numel() < nbytes:
         size = max(nbytes, 1 << 20)
         if buf is not None:
             size = max(size, 2 * buf.numel())
-        buf = torch.zeros(size, dtype=torch.uint8, device=device)
+        buf = torch.zeros(size, dtype=torch.uint8, device=torch.device("cuda", index))
         _ws[key] = buf
     return buf
+
+
+def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    return workspace_on(index, _raw_stream(index), nbytes)

@@ -9,6 +9,8 @@ fallback: host tensors raise.
 
 from __future__ import annotations
 
+import functools
+
 import torch
 
 from . import _lib
@@ -43,35 +45,73 @@ def _check_groups(name: str, scales: torch.Tensor, K: int, N: int, group_size: i
                          f"({K // group_size}, {N}) for K={K}, group_size={group_size}")
 
 
+@functools.lru_cache(maxsize=4096)
+def _ws_bytes(M: int, N: int, K: int) -> int:
+    return int(_lib.load().mm_gemm_workspace_bytes(M, N, K))
+
+
 def _gemm(kind: str, A: torch.Tensor, B_packed: torch.Tensor, scales: torch.Tensor,
           zeros: torch.Tensor | None, group_size: int) -> torch.Tensor:
-    dev = _lib.require_device(A, B_packed, scales, zeros)
-    orig_shape = A.shape
-    K = orig_shape[-1]
-    M = 1
-    for d in orig_shape[:-1]:
-        M *= d
+    fast = _BINDING if _BINDING is not None else _binding()
+    if fast:
+        # checks, output allocation and workspace in C++ (_mmfp4_torch.so)
+        idx = A.get_device()
+        try:
+            return fast.gemm(A, B_packed, scales, zeros if kind == "u4" else None, group_size,
+                             _lib.raw_stream(idx) if idx >= 0 else 0)
+        except RuntimeError as e:
+            if type(e) is RuntimeError and "GPU only" not in str(e):
+                raise _lib.MMError(str(e)) from None
+            raise
+    return _gemm_ctypes(kind, A, B_packed, scales, zeros, group_size)
+
+
+_BINDING = None
+
+
+def _binding():
+    global _BINDING
+    _BINDING = _lib.binding() or False
+    return _BINDING
+
+
+def _gemm_ctypes(kind: str, A: torch.Tensor, B_packed: torch.Tensor, scales: torch.Tensor,
+                 zeros: torch.Tensor | None, group_size: int) -> torch.Tensor:
+    # The per-call host path is kept short: one device check, the current
+    # stream as a raw handle, a cached workspace, no copies of operands that
+    # already have the right dtype and layout.
+    idx = _lib.same_device_index(A, B_packed, scales, zeros)
+    K = A.shape[-1]
+    M = A.numel() // K if K else 0
     K_packed, N = B_packed.shape
     if K_packed * FP4_PER_UINT != K:
         raise ValueError(f"Packed K {K_packed * FP4_PER_UINT} does not match activations K {K}")
-    _check_groups("scales", scales, K, N, group_size)
+    if group_size <= 0 or K % group_size != 0 or scales.shape[0] * group_size != K \
+            or scales.shape[1] != N:
+        _check_groups("scales", scales, K, N, group_size)
     if zeros is not None:
         _check_groups("zeros", zeros, K, N, group_size)
-    a = _half(A.reshape(M, K))
-    b = _packed(B_packed)
-    s = _half(scales)
-    out = torch.empty((M, N), dtype=torch.float16, device=dev)
-    ws_bytes = int(_lib.load().mm_gemm_workspace_bytes(M, N, K))
-    ws = _lib.workspace(dev, ws_bytes)
-    st = _lib.stream_of(a)
+    a = A if A.dtype == torch.float16 and A.is_contiguous() else _half(A)
+    a = a.view(M, K)
+    b = B_packed if B_packed.is_contiguous() else B_packed.contiguous()
+    if b.dtype not in (torch.int32, torch.uint32):
+        raise TypeError(f"packed weights must be int32/uint32 words, got {b.dtype}")
+    s = scales if scales.dtype == torch.float16 and scales.is_contiguous() else _half(scales)
+    out = torch.empty((M, N), dtype=torch.float16, device=a.device)
+    st = _lib.raw_stream(idx)
+    ws = _lib.workspace_on(idx, st, _ws_bytes(M, N, K))
+    if _lib._lib is None:
+        _lib.load()
     if kind == "fp4":
-        _lib.call("mm_fp4_gemm", _lib.ptr(a), _lib.ptr(b), _lib.ptr(s), _lib.ptr(out), M, N, K,
-                  group_size, _lib.ptr(ws), ws.numel(), st)
+        rc = _lib.F.mm_fp4_gemm(a.data_ptr(), b.data_ptr(), s.data_ptr(), out.data_ptr(), M, N,
+                                K, group_size, ws.data_ptr(), ws.numel(), st)
     else:
         z = _half(zeros)
-        _lib.call("mm_u4_gemm", _lib.ptr(a), _lib.ptr(b), _lib.ptr(s), _lib.ptr(z),
-                  _lib.ptr(out), M, N, K, group_size, _lib.ptr(ws), ws.numel(), st)
-    return out.reshape(*orig_shape[:-1], N)
+        rc = _lib.F.mm_u4_gemm(a.data_ptr(), b.data_ptr(), s.data_ptr(), z.data_ptr(),
+                               out.data_ptr(), M, N, K, group_size, ws.data_ptr(), ws.numel(), st)
+    if rc:
+        _lib.check(rc)
+    return out.view(*A.shape[:-1], N)
 
 
 def marlin_gemm_fp4(A: torch.Tensor, B_packed: torch.Tensor, scales: torch.Tensor,

@@ -276,3 +276,31 @@ def test_two_slab_decode_vs_oracle(rng, M, K, N, g, int4):
         out = to_np(mmfp4.marlin_gemm_fp4(to_dev(a), to_dev(packed), to_dev(scales), g))
     assert out.shape == (M, N)
     assert max_abs_rel(out, ref) <= TOL
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 4096, 4096), (37, 512, 256)])
+def test_binding_and_ctypes_paths_agree(M, K, N):
+    """marlin_gemm_fp4 / marlin_gemm_int4 through the per-call C++ binding and
+    through the ctypes path: the same C entry points, bit-identical outputs;
+    errors raise the same exception types."""
+    import mmfp4
+    from mmfp4 import kernels
+    assert kernels._binding(), "the per-call binding (_mmfp4_torch.so) is not built"
+    a, packed, scales, _ = _gpu_problem(M, K, N, 128, seed=4)
+    z = torch.full_like(scales, 8.0)
+    announce(f"binding vs ctypes M={M}")
+    fast = mmfp4.marlin_gemm_fp4(a, packed, scales, 128)
+    fast4 = mmfp4.marlin_gemm_int4(a, packed, scales, z, 128)
+    slow = kernels._gemm_ctypes("fp4", a, packed, scales, None, 128)
+    slow4 = kernels._gemm_ctypes("u4", a, packed, scales, z, 128)
+    assert torch.equal(fast.view(torch.int16), slow.view(torch.int16))
+    assert torch.equal(fast4.view(torch.int16), slow4.view(torch.int16))
+    a3 = a.reshape(1, M, K)
+    assert mmfp4.marlin_gemm_fp4(a3, packed, scales, 128).shape == (1, M, N)
+    for fn in (lambda *x: mmfp4.marlin_gemm_fp4(*x), lambda *x: kernels._gemm_ctypes("fp4", *x[:3], None, x[3])):
+        with pytest.raises(ValueError, match="Packed K"):
+            fn(a[:, :K - 8].contiguous(), packed, scales, 128)
+        with pytest.raises(ValueError):
+            fn(a, packed, scales, 64)
+        with pytest.raises(RuntimeError, match="GPU only"):
+            fn(a.cpu(), packed, scales, 128)
