@@ -78,8 +78,8 @@ struct Pf2Shape {
   static constexpr int A_PIECES = BM * (PF2_BK / 8);   // 16-byte pieces per stage
   static constexpr int B_PIECES = (PF2_BK / 8) * (BN / 4);
   static constexpr int S_PIECES = SROWS * (BN / 8);
-  static_assert(A_PIECES % NTHR == 0 && B_PIECES % 64 == 0 && S_PIECES % 64 == 0, "split");
-  static constexpr int A_IT = A_PIECES / NTHR;
+  static_assert(A_PIECES % 64 == 0 && B_PIECES % 64 == 0 && S_PIECES % 64 == 0, "split");
+  static constexpr int A_IT = (A_PIECES + NTHR - 1) / NTHR;
   static constexpr int B_IT = (B_PIECES + NTHR - 1) / NTHR;
   static constexpr int S_IT = (S_PIECES + NTHR - 1) / NTHR;
   static constexpr int LOADS_PER_CHUNK = A_IT + B_IT + S_IT * (INT4 ? 2 : 1);
@@ -131,7 +131,7 @@ MM_DEV void pf2_mainloop(const Src& src, int K, int g, int c_beg, int c_end, cha
   const f16* a_src[A_IT];
 #pragma unroll
   for (int i = 0; i < A_IT; ++i) {
-    const int p = (i * NWAVE + wave) * 64 + lane;
+    const int p = min((i * NWAVE + wave) * 64 + lane, Sh::A_PIECES - 1);
     const int r = p >> 3, c8 = p & 7;
     a_src[i] = src.arow(r) + 8 * (c8 ^ ((r >> 1) & 7));
   }
@@ -154,8 +154,11 @@ MM_DEV void pf2_mainloop(const Src& src, int K, int g, int c_beg, int c_end, cha
   auto issue = [&](int ch, int st) {
     const int k0 = ch * PF2_BK;
 #pragma unroll
-    for (int i = 0; i < A_IT; ++i)
-      gl2lds16(a_src[i] + k0, smem + st * A_BYTES + (i * NWAVE + wave) * 1024);
+    for (int i = 0; i < A_IT; ++i) {
+      const int wp = i * NWAVE + wave;
+      gl2lds16(a_src[i] + k0,
+               wp * 64 < Sh::A_PIECES ? smem + st * A_BYTES + wp * 1024 : smem + D_OFF);
+    }
 #pragma unroll
     for (int i = 0; i < B_IT; ++i) {
       const int wp = i * NWAVE + wave;
