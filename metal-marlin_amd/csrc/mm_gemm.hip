@@ -580,30 +580,14 @@ k_splitk_reduce(const float* __restrict__ part, int ks, int M, int N, f16* __res
 // ===========================================================================
 // Host-side planning
 // ===========================================================================
-#ifndef MM_SK_NW1
 #define MM_SK_NW1 8         // waves per skinny block, M <= 16 (power of two)
-#endif
-#ifndef MM_SK_NW2
 #define MM_SK_NW2 8         // waves per skinny block, 16 < M <= 32
-#endif
-#ifndef MM_SK_SPW1
 #define MM_SK_SPW1 8        // 32-k steps per wave per round, M <= 16
-#endif
-#ifndef MM_SK_SPW2
 #define MM_SK_SPW2 4        // 32-k steps per wave per round, 16 < M <= 32
-#endif
-#ifndef MM_SK_KS2
 #define MM_SK_KS2 4         // max K split for 16 < M <= 32 (bounds partial traffic)
-#endif
-#ifndef MM_SK_NOSPLIT_TILES
 #define MM_SK_NOSPLIT_TILES 200   // column tiles from which the K range is not split
-#endif
-#ifndef MM_SK_NOSPLIT_TILES1
 #define MM_SK_NOSPLIT_TILES1 96   // the same for M <= 16
-#endif
-#ifndef MM_SK_MAXBLOCKS
 #define MM_SK_MAXBLOCKS 2048
-#endif
 template <int MT> constexpr int sk_nw() { return MT == 1 ? MM_SK_NW1 : MM_SK_NW2; }
 template <int MT> constexpr int sk_spw() { return MT == 1 ? MM_SK_SPW1 : MM_SK_SPW2; }
 // One 64-column virtual-tile quad per block: more column tiles means fewer
@@ -658,10 +642,8 @@ size_t skinny_ws_bytes(int M, int N, int K) {
 // B2/S2/Z2 the up matrix, both [.., N]; the split and workspace are those of
 // the unfused [K, 2N] product (plan_skinny(M, 2N, K)).
 // SK_MULTI: `mp` describes the matrices (N is then mp->ntot, B..Z2 unused).
-#ifndef MM_ROWP_TILES
 #define MM_ROWP_TILES 1      // 64-column tiles per block of the plain row-packed product; 2
                              // measured slower at M=1 (4096x6144 10.1 -> 18.8 us)
-#endif
 template <bool INT4, int MT, int ACT, int ROWP = 0>
 int launch_skinny(const f16* A, int lda, const uint32_t* B, const f16* S, const f16* Z,
                   const uint32_t* B2, const f16* S2, const f16* Z2, f16* C, int ldc, int M,
@@ -708,21 +690,11 @@ int launch_skinny(const f16* A, int lda, const uint32_t* B, const f16* S, const 
   return 0;
 }
 
-#ifndef MM_SK_DUAL
-#define MM_SK_DUAL 1
-#endif
-#ifndef MM_SK_DUAL_SMALL
-#define MM_SK_DUAL_SMALL 1   // also small layers (K*N <= 4096^2) the 64-column plan would split
-#endif
-#ifndef MM_SK_DUAL_NW
 #define MM_SK_DUAL_NW 8
-#endif
 // 64-k steps per wave per round.  Measured at M=1 (qkv / o): 8 waves x 8
 // steps 5.51 / 5.25 us, 8 x 4 5.46 / 5.12, 16 x 4 5.89 / 5.54, 4 x 8
 // 6.12 / 5.79, 4 x 16 5.99 / 5.69.
-#ifndef MM_SK_DUAL_SPW
 #define MM_SK_DUAL_SPW MM_SK_SPW1
-#endif
 // The two-slab kernel serves M <= 8 layers whose 64-column plan runs unsplit
 // on fewer than MM_SK_DUAL_BELOW blocks, when 32-column tiles give at least
 // MM_SK_DUAL_MIN_TILES blocks (measured on MI355X at M=1: 4096 -> 6144
@@ -730,17 +702,13 @@ int launch_skinny(const f16* A, int lda, const uint32_t* B, const f16* S, const 
 // slower as 128 unsplit blocks, 9.3 -> 11.1 us, and keeps the split).  Small
 // layers (K*N <= 4096^2) take it even where the 64-column plan would split:
 // 4096 -> 4096 4.9 us against 5.2-5.3 us for the column-strip kernel.
-#ifndef MM_SK_DUAL_BELOW
 #define MM_SK_DUAL_BELOW 128
-#endif
-#ifndef MM_SK_DUAL_MIN_TILES
 #define MM_SK_DUAL_MIN_TILES 96
-#endif
 
 bool use_dual(int M, int N, int K, int g) {
-  if (!MM_SK_DUAL || M > 8 || K % 64 != 0 || g % 64 != 0 || N % 4 != 0) return false;
+  if (M > 8 || K % 64 != 0 || g % 64 != 0 || N % 4 != 0) return false;
   if (flush_steps(g / 2, MM_SK_DUAL_SPW) == 0) return false;
-  return (plan_skinny(M, N, K).ksplit == 1 || (MM_SK_DUAL_SMALL && (long)K * N <= 4096L * 4096)) &&
+  return (plan_skinny(M, N, K).ksplit == 1 || (long)K * N <= 4096L * 4096) &&
          mm_cdiv(N, SK_COLS) < MM_SK_DUAL_BELOW && mm_cdiv(N, 32) >= MM_SK_DUAL_MIN_TILES;
 }
 
@@ -766,22 +734,12 @@ int launch_dual(const f16* A, const uint32_t* B, const f16* S, const f16* Z, f16
   return 0;
 }
 
-// Row-packed two-slab kernel: 0 never, 1 on the shapes use_dual picks, 2 for
-// every M <= 8 (measured slower outside use_dual's shapes at M=1:
-// 4096x28672 18.7 -> 20.9 us, 14336x4096 12.4 -> 16.7 us).
-#ifndef MM_ROWP_DUAL
-#define MM_ROWP_DUAL 1
-#endif
+// The row-packed product takes the two-slab kernel on the shapes use_dual
+// picks (measured slower on the others at M=1: 4096x28672 18.7 -> 20.9 us,
+// 14336x4096 12.4 -> 16.7 us).
 
-#ifndef MM_ST_NW
 #define MM_ST_NW 8
-#endif
-#ifndef MM_ST_SPW
 #define MM_ST_SPW 8
-#endif
-#ifndef MM_ST_MODE
-#define MM_ST_MODE 1        // 0: never, 1: heuristic, 2: always (M <= 16, g % 32 == 0)
-#endif
 
 template <bool INT4, int NS>
 int launch_strip(const f16* A, int lda, const uint32_t* B, const f16* S, const f16* Z, f16* C,
@@ -817,26 +775,12 @@ int launch_prefill(const f16* A, int lda, const uint32_t* B, const f16* S, const
 }
 
 
-#ifndef MM_PF2_ENABLE
-#define MM_PF2_ENABLE 1
-#endif
 // (WM, WN, RB, CW) of the pipelined prefill tiles.
-#ifndef PF2_BIG
 #define PF2_BIG 2, 4, 4, 2       // 256 x 256, 8 waves of 128 x 64
-#endif
-#ifndef PF2_BIG_PLAIN
-#define PF2_BIG_PLAIN PF2_BIG  // the plain product's 256 x 256 tile
-#endif
-#ifndef PF2_MID
 #define PF2_MID 2, 4, 2, 2       // 128 x 256, 8 waves of 64 x 64
-#endif
-#ifndef PF2_SMALL
 #define PF2_SMALL 1, 4, 2, 2     // 64 x 256, 4 waves of 64 x 64
-#endif
 
-#ifndef MM_PF_KS_BLOCKS
 #define MM_PF_KS_BLOCKS 200   // split K while the grid has fewer blocks than this
-#endif
 // Prefill plan: tile config (0: 256x256, 1: 128x256, 2: 64x256) and K split.
 struct PrefillPlan {
   int cfg;
@@ -903,11 +847,11 @@ int gemm_dispatch(const char* who, const f16* A, const uint32_t* B, const f16* S
   // larger matrices take the prefill kernels (64-bit addressing) at any M.
   const bool off32 = (size_t)(K / 8) * (size_t)N * 4 < ((size_t)1 << 32);
   if (off32 && use_dual(M, N, K, g)) return launch_dual<INT4>(A, B, S, Z, C, M, N, K, g, st);
-  if (off32 && MM_ST_MODE && M <= 16 && flush_steps(g, MM_ST_SPW) > 0) {
+  if (off32 && M <= 16 && flush_steps(g, MM_ST_SPW) > 0) {
     // Column strips (no split-K hand-off) win for small layers, where the
     // hand-off is a large share of the launch; split-K wins from ~13 MB up
     // (measured on MI355X: 4096x4096 5.8 vs 7.0 us, 4096x6144 8.0 vs 7.2 us).
-    if (MM_ST_MODE == 2 || ((long)K * N <= 4096L * 4096 && N / 16 >= 128))
+    if ((long)K * N <= 4096L * 4096 && N / 16 >= 128)
       return launch_strip<INT4, 1>(A, K, B, S, Z, C, N, M, N, K, g, st);
   }
   if (off32 && M <= 16)
@@ -918,7 +862,7 @@ int gemm_dispatch(const char* who, const f16* A, const uint32_t* B, const f16* S
                                             K, g, ws, ws_bytes, st);
   // The pipelined kernel stages scale rows in 8-column pieces (N % 8 == 0)
   // and whole 64-k chunks (K % 64 == 0).
-  if (MM_PF2_ENABLE && N % 8 == 0 && K % PF2_BK == 0) {
+  if (N % 8 == 0 && K % PF2_BK == 0) {
     const PrefillPlan p = plan_prefill(M, N, K);
     float* part = nullptr;
     if (p.ksplit > 1) {
@@ -930,7 +874,7 @@ int gemm_dispatch(const char* who, const f16* A, const uint32_t* B, const f16* S
     }
     switch (p.cfg) {
       case 0:
-        return launch_prefill2<INT4, SK_PLAIN, PF2_BIG_PLAIN>(A, K, B, S, Z, nullptr, nullptr, nullptr,
+        return launch_prefill2<INT4, SK_PLAIN, PF2_BIG>(A, K, B, S, Z, nullptr, nullptr, nullptr,
                                                         C, N, M, N, K, g, p.ksplit, part, st);
       case 1:
         return launch_prefill2<INT4, SK_PLAIN, PF2_MID>(A, K, B, S, Z, nullptr, nullptr, nullptr,
@@ -1093,7 +1037,7 @@ extern "C" int mm_fp4_gemm_rowpacked(const uint16_t* A, const uint32_t* B, const
                "scales 8-byte)", who);
   if (M == 0) return 0;
   hipStream_t st = (hipStream_t)stream;
-  if (MM_ROWP_DUAL && K % 512 == 0 && M <= 8 && (MM_ROWP_DUAL == 2 || use_dual(M, N, K, g))) {
+  if (K % 512 == 0 && M <= 8 && use_dual(M, N, K, g)) {
     // Two-slab kernel, 32-column blocks over the whole K (the shapes the
     // Marlin-layout path also gives it).
     constexpr int NW = 8;

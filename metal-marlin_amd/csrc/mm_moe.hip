@@ -18,12 +18,8 @@ namespace {
 using namespace mmsk;
 using namespace mmpf;
 
-#ifndef MM_MOE_DEC_NW
 #define MM_MOE_DEC_NW 4      // waves per block of the grouped decode kernel (busy launches)
-#endif
-#ifndef MM_MOE_DEC_SPW
 #define MM_MOE_DEC_SPW 4     // 32-k steps per wave per round there
-#endif
 // Grouped prefill kernel: a 2-stage LDS ring (loads one chunk ahead) and at
 // most 168 VGPRs, so three 4-wave blocks fit per CU (3 waves per SIMD).
 // Measured on MI355X at the Qwen3-30B-A3B shapes: the more resident waves hide
@@ -32,9 +28,7 @@ using namespace mmpf;
 // 282 -> 264 us; down at T=512 40 -> 33 us.
 constexpr int MOE_PF_STAGES = 2;
 constexpr int MOE_PF_WAVES_PER_SIMD = 3;
-#ifndef MM_MOE_PF_ROWS
 #define MM_MOE_PF_ROWS 24   // average rows per expert above which the MFMA tile kernel runs
-#endif
 
 // Expert weights: experts e < Er are slices of the stacked [Er, K/8, N]
 // words and [Er, K/g, N] scales; expert Er (when a shared expert is run as an

@@ -30,15 +30,8 @@
 #include "mm_common.h"
 #include "mm_skinny.h"
 
-#ifndef MM_PF2_SCHED
-#define MM_PF2_SCHED 1
-#endif
-#ifndef MM_PF2_SCHED_DS
 #define MM_PF2_SCHED_DS 3
-#endif
-#ifndef MM_PF2_SCHED_VALU
 #define MM_PF2_SCHED_VALU 9
-#endif
 namespace mmpf {
 using namespace mmsk;
 
@@ -292,14 +285,12 @@ MM_DEV void pf2_mainloop(const Src& src, int K, int g, int c_beg, int c_end, cha
       // decode VALU so the matrix pipe never drains while they issue.  Up to
       // 3 LDS reads and 9 VALU ops after each MFMA (front-loading the next
       // step's operands) measured 2-6% faster than 1 and 3 at M = 512..8192.
-#if MM_PF2_SCHED > 0
 #pragma unroll
       for (int i = 0; i < RBL * CW; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
         __builtin_amdgcn_sched_group_barrier(0x100, MM_PF2_SCHED_DS, 0);   // DS read
         __builtin_amdgcn_sched_group_barrier(0x002, MM_PF2_SCHED_VALU, 0);   // VALU
       }
-#endif
     }
   };
   // The ring position of chunk ch is (ch - c_beg) % STAGES: unroll by STAGES so

@@ -23,9 +23,6 @@
 // the activations, scales and the following launches (measured on MI355X:
 // Llama-3-8B layer at M=1 35.5 -> 33.8 us per step; the MoE decode MLP at
 // T=32 70 -> 65 us).  Scale rows gain nothing from it and stay cached.
-#ifndef MM_SK_NT
-#define MM_SK_NT 1
-#endif
 namespace mmsk {
 
 constexpr int SK_COLS = 64;   // columns of one virtual-tile quad
@@ -175,8 +172,8 @@ MM_DEV void skinny_wave(const f16* __restrict__ A, int lda, const int* __restric
       const int kp = min(4 * (SLAB * min(stb + i, nsteps - 1) + hs) + q, KP - 1);
 #pragma unroll
       for (int t = 0; t < NT; ++t)
-        w[i][t] = MM_SK_NT ? __builtin_nontemporal_load(at_bytes<u32x4>(tl[t].B, ((uint32_t)kp * (uint32_t)N + coff[t]) * 4u))
-                           : *at_bytes<u32x4>(tl[t].B, ((uint32_t)kp * (uint32_t)N + coff[t]) * 4u);
+        w[i][t] = __builtin_nontemporal_load(
+            at_bytes<u32x4>(tl[t].B, ((uint32_t)kp * (uint32_t)N + coff[t]) * 4u));
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
         a[i][mt] = *at_bytes<f16x8>(A, aoff[mt] + (uint32_t)kp * 16u);
@@ -451,8 +448,8 @@ MM_DEV void strip_wave(const f16* __restrict__ A, int lda, const int* __restrict
       const int kp = min(4 * min(slb + u, nsl - 1) + kb, KP - 1);
 #pragma unroll
       for (int t = 0; t < NS; ++t)
-        R.w[u][t] = MM_SK_NT ? __builtin_nontemporal_load(at_bytes<uint32_t>(B, ((uint32_t)kp * (uint32_t)N + bcol[t]) * 4u))
-                             : *at_bytes<uint32_t>(B, ((uint32_t)kp * (uint32_t)N + bcol[t]) * 4u);
+        R.w[u][t] = __builtin_nontemporal_load(
+            at_bytes<uint32_t>(B, ((uint32_t)kp * (uint32_t)N + bcol[t]) * 4u));
       R.a[u] = *at_bytes<f16x8>(A, aoff + (uint32_t)kp * 16u);
     }
   };
