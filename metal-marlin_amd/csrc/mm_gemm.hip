@@ -690,6 +690,32 @@ int launch_skinny(const f16* A, int lda, const uint32_t* B, const f16* S, const 
   return 0;
 }
 
+// Plain skinny product with two 64-column tiles per block and the whole K
+// range per block (no split, so no workspace is touched).  The caller
+// guarantees at least MM_SK_NOSPLIT_TILES blocks.
+template <bool INT4, int MT>
+int launch_skinny_nt2(const f16* A, const uint32_t* B, const f16* S, const f16* Z, f16* C, int M,
+                      int N, int K, int g, hipStream_t st) {
+  constexpr int NT = 2, SPW = sk_spw<MT>(), NW = sk_nw<MT>();
+  const int nrounds = mm_cdiv((K / 8 + 3) / 4, NW * SPW);
+  const dim3 grid(mm_cdiv(N, NT * SK_COLS), 1);
+  const SkMulti none{};
+#define MM_LAUNCH_SKN(FLV)                                                                    \
+  hipLaunchKernelGGL((k_skinny<INT4, MT, NT, SPW, NW, FLV, SK_PLAIN, 0>), grid, dim3(NW * 64), \
+                     0, st, A, K, B, S, Z, nullptr, nullptr, nullptr, C, N, M, N, K, g,         \
+                     nrounds, nullptr, nullptr, none)
+  switch (flush_steps(g, SPW)) {
+    case 1: MM_LAUNCH_SKN(1); break;
+    case 2: MM_LAUNCH_SKN(2); break;
+    case 4: MM_LAUNCH_SKN(4 <= SPW ? 4 : 0); break;
+    case 8: MM_LAUNCH_SKN(8 <= SPW ? 8 : 0); break;
+    default: MM_LAUNCH_SKN(0); break;
+  }
+#undef MM_LAUNCH_SKN
+  MM_CHECK_LAUNCH("gemm(skinny, 128-column blocks)");
+  return 0;
+}
+
 #define MM_SK_DUAL_NW 8
 // 64-k steps per wave per round.  Measured at M=1 (qkv / o): 8 waves x 8
 // steps 5.51 / 5.25 us, 8 x 4 5.46 / 5.12, 16 x 4 5.89 / 5.54, 4 x 8
@@ -853,6 +879,14 @@ int gemm_dispatch(const char* who, const f16* A, const uint32_t* B, const f16* S
     // (measured on MI355X: 4096x4096 5.8 vs 7.0 us, 4096x6144 8.0 vs 7.2 us).
     if ((long)K * N <= 4096L * 4096 && N / 16 >= 128)
       return launch_strip<INT4, 1>(A, K, B, S, Z, C, N, M, N, K, g, st);
+  }
+  // Wide layers at 9..32 rows: 128-column blocks (NT = 2) with no K split.  The
+  // activation rows each block reads are then shared by twice the weight
+  // columns (measured on MI355X, 4096 x 28672: M=16 16.5 -> 15.0 us, M=32
+  // 24.6 -> 20.4 us; at M <= 8 and on narrower layers the 64-column plan wins).
+  if (off32 && M > 8 && M <= 32 && mm_cdiv(N, 2 * SK_COLS) >= MM_SK_NOSPLIT_TILES) {
+    if (M <= 16) return launch_skinny_nt2<INT4, 1>(A, B, S, Z, C, M, N, K, g, st);
+    return launch_skinny_nt2<INT4, 2>(A, B, S, Z, C, M, N, K, g, st);
   }
   if (off32 && M <= 16)
     return launch_skinny<INT4, 1, SK_PLAIN>(A, K, B, S, Z, nullptr, nullptr, nullptr, C, N, M, N,

@@ -74,7 +74,9 @@ DENSE = [
     (1, 4096, 28672, 128, "k_skinny unsplit"),
     (1, 14336, 4096, 128, "k_skinny split-K"),
     (13, 14336, 4096, 64, "k_skinny split-K M=13"),
-    (24, 4096, 28672, 128, "k_skinny MT=2"),
+    (24, 4096, 28672, 128, "k_skinny MT=2, 128-column blocks"),
+    (12, 4096, 28672, 64, "k_skinny MT=1, 128-column blocks"),
+    (32, 4096, 6144, 128, "k_skinny MT=2 split-K, 64-column blocks"),
     (32, 14336, 4096, 128, "k_skinny MT=2 split-K"),
     (64, 4096, 1024, 128, "k_prefill2 64-row tile"),
     (128, 14336, 4096, 128, "k_prefill2 split-K + reduce"),
@@ -95,8 +97,8 @@ def test_fp4_gemm_bit_exact(rng, M, K, N, g, family):
     _same(mmfp4.marlin_gemm_fp4(to_dev(a), to_dev(packed), to_dev(scales), g), ref)
 
 
-@pytest.mark.parametrize("M,K,N,g,family", [d for d in DENSE if d[0] in (1, 12, 13, 24, 64, 128,
-                                                                          100)])
+@pytest.mark.parametrize("M,K,N,g,family", [d for d in DENSE if d[0] in (1, 12, 13, 24, 32, 64,
+                                                                          128, 100)])
 def test_u4_gemm_bit_exact(rng, M, K, N, g, family):
     import mmfp4
     packed, s, z = _exact_u4(rng, K, N, g)
