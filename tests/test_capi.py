@@ -78,3 +78,21 @@ def test_host_tensors_are_refused():
         mmfp4.marlin_gemm_fp4(a, b, s, 32)
     with pytest.raises(RuntimeError, match="GPU only"):
         mmfp4.dequant_fp4(b, s, 64, 64, 32)
+
+
+def test_new_entry_points_validate():
+    with pytest.raises(ValueError, match="group_size"):
+        _lib.call("mm_fp4_flat_quantize", None, 16, 0, 0, None, None, None)
+    with pytest.raises(ValueError, match="dtype"):
+        _lib.call("mm_fp4_flat_quantize", None, 16, 5, 8, None, None, None)
+    with pytest.raises(ValueError, match="cover fewer"):
+        _lib.call("mm_fp4_flat_dequantize", None, None, 300, 2, 128, None, None)
+    with pytest.raises(ValueError, match="scales_layout"):
+        _lib.call("mm_fp4_gemm_rowpacked", None, None, None, None, 1, 64, 256, 64, 2, None, 0,
+                  None)
+    with pytest.raises(ValueError, match="built-in scratch"):
+        _lib.call("mm_fp4_gemm_noalloc", None, None, None, None, 256, 4096, 4096, 128, None)
+    with pytest.raises(ValueError, match="shared expert"):
+        _lib.call("mm_moe_mlp_shared_fp4", None, None, 0, None, 4, 2, 8, 256, 128, None, None,
+                  None, None, None, None, None, None, ctypes.c_float(1.0), None, 128, None, None,
+                  None, None, None)
