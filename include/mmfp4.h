@@ -76,9 +76,11 @@ int mm_fp4_gemm(const uint16_t* A, const uint32_t* B, const uint16_t* scales, ui
  * B [N, K/8] uint32 (word (n, kp) holds k = 8kp .. 8kp+7 of row n), scales
  * fp16 [K/g, N] (scales_layout = 0, the layer's canonical [n_groups, N]) or
  * [N, K/g] (scales_layout = 1, the transposed layout the layer also accepts,
- * metal_marlin/layers/mmfp4_linear.py:53-86).  Decode sizes only: M <= 16,
- * K % 256 == 0, g % 64 == 0, N % 4 == 0; weights and scales are read in place
- * (no transpose).  Workspace as mm_gemm_workspace_bytes(M, N, K).  Replaces
+ * metal_marlin/layers/mmfp4_linear.py:53-86).  K % 256 == 0, g % 64 == 0,
+ * N % 4 == 0; M <= 16 runs the decode kernels, larger M the pipelined prefill
+ * kernel, which needs N % 8 == 0 and scales_layout 0.  Weights and scales are
+ * read in place at every M (no transpose).  Workspace as
+ * mm_gemm_workspace_bytes(M, N, K).  Replaces
  * metal_marlin/layers/mmfp4_linear.py:549-598 (mmfp4_gemm), which transposes
  * the row-packed words to the [K/8, N] layout on every call (:414-478). */
 int mm_fp4_gemm_rowpacked(const uint16_t* A, const uint32_t* B, const uint16_t* scales,

@@ -15,6 +15,7 @@
 //    (deterministic order, counter left at zero for the next call).
 //  * prefill (M > 32): 32x32x16 MFMA tiles, A double-buffered through LDS,
 //    B loaded as packed words one chunk ahead and dequantised in registers.
+#include <algorithm>
 #include <mutex>
 #include <type_traits>
 
@@ -458,6 +459,22 @@ struct DenseSrc {
   MM_DEV const f16* zcol(int P, int w) const { return Z + min(n0 + P, N - w); }
 };
 
+// Row-packed FP4 weights B [N, K/8] (kp = K/8 words per column), scales
+// [K/g, N] as DenseSrc.
+struct DenseRowSrc {
+  static constexpr bool kRowPacked = true;
+  const f16* A;
+  int lda, M, m0, N, n0;
+  const uint32_t* B;
+  const f16* S;
+  const f16* Z;
+  int ld, kp;
+  MM_DEV const f16* arow(int r) const { return A + (size_t)min(m0 + r, M - 1) * lda; }
+  MM_DEV const uint32_t* brow(int P) const { return B + (size_t)min(n0 + P, N - 1) * kp; }
+  MM_DEV const f16* scol(int P, int w) const { return S + min(n0 + P, N - w); }
+  MM_DEV const f16* zcol(int P, int w) const { return Z + min(n0 + P, N - w); }
+};
+
 // Gate/up pair: (B, S, Z) gate and (B2, S2, Z2) up matrices, both [.., N];
 // n0 is the block's first output column.
 struct PairSrc {
@@ -478,7 +495,8 @@ struct PairSrc {
   }
 };
 
-template <bool INT4, int WM, int WN, int RB, int CW, bool G64, int ACT>
+// ROWS: B is row-packed [N, K/8] (SK_PLAIN only).
+template <bool INT4, int WM, int WN, int RB, int CW, bool G64, int ACT, bool ROWS = false>
 __global__ void __launch_bounds__(WM * WN * 64)
 k_prefill2(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
            const f16* __restrict__ S, const f16* __restrict__ Z, const uint32_t* __restrict__ B2,
@@ -490,6 +508,7 @@ k_prefill2(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
   // columns and tile 1 the same 32 up columns, so a block covers BN/2 output
   // columns.  Requires K % 64 == 0 and N % 8 == 0 (checked by the host).
   static_assert(ACT == SK_PLAIN || CW == 2, "pair modes pair two column tiles");
+  static_assert(!ROWS || (ACT == SK_PLAIN && !INT4), "row-packed weights: plain FP4 product");
   constexpr int SROWS = G64 ? PF2_SROWS_G64 : PF2_SROWS;
   using Sh = Pf2Shape<INT4, WM, WN, RB, CW, PF2_STAGES, SROWS>;
   __shared__ __attribute__((aligned(16))) char smem[Sh::LDS_BYTES];
@@ -505,7 +524,11 @@ k_prefill2(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
   const int c_beg = blockIdx.z * cps;
   const int c_end = min(nch_all, c_beg + cps);
   f32x16 acc[RB][CW];
-  if constexpr (ACT == SK_PLAIN) {
+  if constexpr (ROWS) {
+    const DenseRowSrc src{A, lda, M, m0, N, n0, B, S, Z, N, K / 8};
+    pf2_mainloop<INT4, WM, WN, RB, CW, G64, false, PF2_STAGES, SROWS>(src, K, g, c_beg, c_end,
+                                                                  smem, acc);
+  } else if constexpr (ACT == SK_PLAIN) {
     const DenseSrc src{A, lda, M, m0, N, n0, B, S, Z, N};
     pf2_mainloop<INT4, WM, WN, RB, CW, G64, false, PF2_STAGES, SROWS>(src, K, g, c_beg, c_end,
                                                                   smem, acc);
@@ -833,16 +856,17 @@ size_t prefill_ws_bytes(int M, int N, int K) {
   return p.ksplit > 1 ? (size_t)p.ksplit * M * N * sizeof(float) : 0;
 }
 
-template <bool INT4, int ACT, int WM, int WN, int RB, int CW>
+template <bool INT4, int ACT, int WM, int WN, int RB, int CW, bool ROWS = false>
 int launch_prefill2(const f16* A, int lda, const uint32_t* B, const f16* S, const f16* Z,
                     const uint32_t* B2, const f16* S2, const f16* Z2, f16* C, int ldc, int M,
                     int N, int K, int g, int ks, float* part, hipStream_t st) {
   constexpr int BM = WM * 32 * RB, BN = WN * 32 * CW;
   dim3 grid(mm_cdiv(N, ACT == SK_PLAIN ? BN : BN / 2), mm_cdiv(M, BM), ks);
   if (g % PF2_BK == 0)
-    hipLaunchKernelGGL((k_prefill2<INT4, WM, WN, RB, CW, true, ACT>), grid, dim3(WM * WN * 64), 0,
-                       st, A, lda, B, S, Z, B2, S2, Z2, C, ldc, M, N, K, g, part);
-  else
+    hipLaunchKernelGGL((k_prefill2<INT4, WM, WN, RB, CW, true, ACT, ROWS>), grid,
+                       dim3(WM * WN * 64), 0, st, A, lda, B, S, Z, B2, S2, Z2, C, ldc, M, N, K, g,
+                       part);
+  else if constexpr (!ROWS)
     hipLaunchKernelGGL((k_prefill2<INT4, WM, WN, RB, CW, false, ACT>), grid, dim3(WM * WN * 64),
                        0, st, A, lda, B, S, Z, B2, S2, Z2, C, ldc, M, N, K, g, part);
   MM_CHECK_LAUNCH("gemm(prefill2)");
@@ -1039,6 +1063,9 @@ int multi_dispatch(const char* who, const f16* A, int nmat, const uint32_t* cons
 extern "C" size_t mm_gemm_workspace_bytes(int M, int N, int K) {
   if (M <= 0 || N <= 0 || K <= 0) return SK_COUNTER_BYTES;
   if (M > 32) return SK_COUNTER_BYTES + prefill_ws_bytes(M, N, K);
+  // 17..32 rows: enough for the prefill kernel too (the row-packed product
+  // takes it from 17 rows).
+  if (M > 16) return std::max(skinny_ws_bytes(M, N, K), SK_COUNTER_BYTES + prefill_ws_bytes(M, N, K));
   return skinny_ws_bytes(M, N, K);
 }
 
@@ -1055,14 +1082,15 @@ extern "C" int mm_fp4_gemm_rowpacked(const uint16_t* A, const uint32_t* B, const
   MM_CHECK_ARG(scales_layout == 0 || scales_layout == 1,
                "%s: scales_layout=%d must be 0 ([K/g, N]) or 1 ([N, K/g])", who, scales_layout);
   MM_CHECK_ARG(M >= 0 && N > 0 && K > 0, "%s: bad shape M=%d N=%d K=%d", who, M, N, K);
-  MM_CHECK_ARG(M <= 16, "%s: M=%d: the row-packed decode kernel takes M <= 16 (larger M: "
-               "transpose to the [K/8, N] layout and call mm_fp4_gemm)", who, M);
+  MM_CHECK_ARG(M <= 16 || scales_layout == 0,
+               "%s: M=%d: above 16 rows the scales must be [K/g, N] (scales_layout 0)", who, M);
+  MM_CHECK_ARG(M <= 16 || N % 8 == 0, "%s: N=%d must be divisible by 8 for M > 16", who, N);
   MM_CHECK_ARG(K % 256 == 0, "%s: K=%d must be divisible by 256", who, K);
   MM_CHECK_ARG(g > 0 && g % 64 == 0 && K % g == 0,
                "%s: group_size=%d must be a multiple of 64 dividing K=%d", who, g, K);
   MM_CHECK_ARG(N % 4 == 0, "%s: N=%d must be divisible by 4", who, N);
-  MM_CHECK_ARG((size_t)N * (size_t)(K / 8) * 4 < ((size_t)1 << 32),
-               "%s: the packed weights must be under 4 GiB", who);
+  MM_CHECK_ARG(M > 16 || (size_t)N * (size_t)(K / 8) * 4 < ((size_t)1 << 32),
+               "%s: the packed weights must be under 4 GiB at M <= 16", who);
   // [K/g, N] scales are read as 4 adjacent columns (8 bytes) per lane.
   const uintptr_t salign = scales_layout == 0 ? 7 : 1;
   MM_CHECK_ARG(((uintptr_t)A & 15) == 0 && ((uintptr_t)B & 15) == 0 &&
@@ -1071,6 +1099,34 @@ extern "C" int mm_fp4_gemm_rowpacked(const uint16_t* A, const uint32_t* B, const
                "scales 8-byte)", who);
   if (M == 0) return 0;
   hipStream_t st = (hipStream_t)stream;
+  if (M > 16) {
+    // Pipelined prefill kernel reading the row-packed words in place.
+    const PrefillPlan p = plan_prefill(M, N, K);
+    float* part = nullptr;
+    if (p.ksplit > 1) {
+      const size_t need = SK_COUNTER_BYTES + prefill_ws_bytes(M, N, K);
+      MM_CHECK_ARG(ws != nullptr && ws_bytes >= need,
+                   "%s: workspace of %zu bytes is smaller than the %zu required", who, ws_bytes,
+                   need);
+      part = (float*)((char*)ws + SK_COUNTER_BYTES);
+    }
+    const f16* a = (const f16*)A;
+    const f16* s = (const f16*)S;
+    switch (p.cfg) {
+      case 0:
+        return launch_prefill2<false, SK_PLAIN, PF2_BIG, true>(
+            a, K, B, s, nullptr, nullptr, nullptr, nullptr, (f16*)C, N, M, N, K, g, p.ksplit,
+            part, st);
+      case 1:
+        return launch_prefill2<false, SK_PLAIN, PF2_MID, true>(
+            a, K, B, s, nullptr, nullptr, nullptr, nullptr, (f16*)C, N, M, N, K, g, p.ksplit,
+            part, st);
+      default:
+        return launch_prefill2<false, SK_PLAIN, PF2_SMALL, true>(
+            a, K, B, s, nullptr, nullptr, nullptr, nullptr, (f16*)C, N, M, N, K, g, p.ksplit,
+            part, st);
+    }
+  }
   if (K % 512 == 0 && M <= 8 && use_dual(M, N, K, g)) {
     // Two-slab kernel, 32-column blocks over the whole K (the shapes the
     // Marlin-layout path also gives it).

@@ -8,7 +8,8 @@
 //   A stage: BM rows x 64 halves, 16-byte pieces XOR-swizzled by row
 //            (piece (r, c8) lives at r*8 + (c8 ^ ((r >> 1) & 7))) so the MFMA
 //            operand reads of 32 consecutive rows spread over the banks;
-//   B stage: 8 word rows x BN LDS columns of packed words;
+//   B stage: 8 word rows x BN LDS columns of packed words (row-packed
+//            weights: 16-byte pieces of a column's 8 words, see below);
 //   S stage: up to 8 scale rows x BN fp16 (the groups the chunk touches),
 //   Z stage: same for INT4 zero points.
 // Every thread issues the same number of loads per chunk (addresses are
@@ -41,6 +42,15 @@ constexpr int PF2_STAGES = 3;   // default LDS ring depth: loads run STAGES-1 ch
 // g = 8); with g % 64 == 0 a chunk lies in one group and 2 rows suffice.
 constexpr int PF2_SROWS = 8;
 constexpr int PF2_SROWS_G64 = 2;
+
+// A source whose weights are row-packed (`kRowPacked`, [N, K/8] words: a
+// column's 8 words of a 64-k chunk are 32 contiguous bytes) provides brow(P),
+// word 0 of the column behind LDS column P, in place of bcol.
+template <class S, class = void>
+struct is_rowpacked : std::false_type {};
+template <class S>
+struct is_rowpacked<S, std::void_t<decltype(S::kRowPacked)>>
+    : std::integral_constant<bool, S::kRowPacked> {};
 
 template <class F, int... I>
 MM_DEV void static_for(F&& f, std::integer_sequence<int, I...>) {
@@ -128,11 +138,27 @@ MM_DEV void pf2_mainloop(const Src& src, int K, int g, int c_beg, int c_end, cha
     const int r = p >> 3, c8 = p & 7;
     a_src[i] = src.arow(r) + 8 * (c8 ^ ((r >> 1) & 7));
   }
+  // Marlin-layout B: piece p is 4 columns of one word row; the stage holds
+  // [8 word rows][BN columns].  Row-packed B (ROWP): piece p is 4 words (16
+  // bytes) of one column, half hf = words 4hf..4hf+3; the stage holds
+  // [CW][BN/CW][2 halves] pieces, column P = CW*c + j at slot
+  // 2*(j*(BN/CW) + c) + hf.  A load instruction then reads both halves (32
+  // contiguous bytes) of 32 columns, and the 16 lanes of an LDS read pass
+  // read every other piece of a 512-byte span.  Both layouts are loaded
+  // global -> LDS directly.
+  constexpr bool ROWP = is_rowpacked<Src>::value;
+  static_assert(!ROWP || (G64 && !TM), "row-packed B: one group per chunk, adjacent columns");
   const uint32_t* b_src[B_IT];
 #pragma unroll
   for (int i = 0; i < B_IT; ++i) {
     const int p = min((i * NWAVE + wave) * 64 + lane, Sh::B_PIECES - 1);
-    b_src[i] = src.bcol(4 * (p % (BN / 4)), 4) + (size_t)(p / (BN / 4)) * ld;
+    if constexpr (ROWP) {
+      const int hf = p % 2, rem = p / 2;     // B_PIECES == 2 * BN
+      const int j = rem / (BN / CW), c = rem % (BN / CW);
+      b_src[i] = src.brow(c * CW + j) + 4 * hf;
+    } else {
+      b_src[i] = src.bcol(4 * (p % (BN / 4)), 4) + (size_t)(p / (BN / 4)) * ld;
+    }
   }
   int s_row[S_IT];
   const f16* s_src[S_IT];
@@ -155,7 +181,7 @@ MM_DEV void pf2_mainloop(const Src& src, int K, int g, int c_beg, int c_end, cha
 #pragma unroll
     for (int i = 0; i < B_IT; ++i) {
       const int wp = i * NWAVE + wave;
-      gl2lds16(b_src[i] + (size_t)(k0 / 8) * ld,
+      gl2lds16(b_src[i] + (ROWP ? (size_t)(k0 / 8) : (size_t)(k0 / 8) * ld),
                wp * 64 < Sh::B_PIECES ? smem + B_OFF + st * B_BYTES + wp * 1024 : smem + D_OFF);
     }
     const int gi0 = k0 / g;
@@ -185,10 +211,17 @@ MM_DEV void pf2_mainloop(const Src& src, int K, int g, int c_beg, int c_end, cha
   constexpr int CSTEP = TM ? 32 : 1;                                   // tile j: + j*CSTEP
   const int arow = wm * 32 * RB + l32;               // lane's row in row block 0
   const int hx = h ^ ((arow >> 1) & 7);              // rows of all row blocks share (r>>1)&7
+  // MFMA step t covers, in lane half h, the k of word row 2t + h (Marlin
+  // B) or 4h + t (ROWP B: a lane's four steps then use the 4 words of one
+  // piece); the A piece read is the one holding those 8 k.
   uint32_t a_off[PF2_BK / 16];                       // + st*A_BYTES + rb*32*128
 #pragma unroll
-  for (int t = 0; t < PF2_BK / 16; ++t) a_off[t] = arow * 128 + ((2 * t) ^ hx) * 16;
-  const uint32_t b_off = B_OFF + (h * BN + colw) * 4;   // + st*B_BYTES + t*2*BN*4
+  for (int t = 0; t < PF2_BK / 16; ++t)
+    a_off[t] = ROWP ? arow * 128 + ((4 * h + t) ^ ((arow >> 1) & 7)) * 16
+                    : arow * 128 + ((2 * t) ^ hx) * 16;
+  // + st*B_BYTES, and + t*2*BN*4 (Marlin) or + j*(BN/CW)*32 (ROWP)
+  const uint32_t b_off = ROWP ? B_OFF + ((wn * 32 + l32) * 2 + h) * 16
+                              : B_OFF + (h * BN + colw) * 4;
   typedef uint32_t wvec __attribute__((ext_vector_type(CW)));
   typedef f16 svec __attribute__((ext_vector_type(CW)));
   auto read_w = [&](uint32_t off) {
@@ -229,6 +262,12 @@ MM_DEV void pf2_mainloop(const Src& src, int K, int g, int c_beg, int c_end, cha
     // G64: the chunk lies in one group, so its scale (zero) row is read and
     // sanitised once; otherwise each step reads the row of its own group.
     svec sc = {}, nzc = {};
+    u32x4 bp[ROWP ? CW : 1];   // ROWP: the lane's piece of each column tile
+    if constexpr (ROWP) {
+#pragma unroll
+      for (int j = 0; j < CW; ++j)
+        bp[j] = *(const u32x4*)(smem + b_off + st * B_BYTES + j * (BN / CW) * 32);
+    }
     if constexpr (G64) {
       const svec s0 = read_s(S_OFF + st * S_BYTES + colw * 2);
 #pragma unroll
@@ -240,7 +279,12 @@ MM_DEV void pf2_mainloop(const Src& src, int K, int g, int c_beg, int c_end, cha
       }
     }
     auto frag = [&](int t, int slot) {
-      wv[slot] = read_w(b_off + st * B_BYTES + t * 2 * BN * 4);
+      if constexpr (ROWP) {
+#pragma unroll
+        for (int j = 0; j < CW; ++j) wv[slot][j] = bp[j][t];
+      } else {
+        wv[slot] = read_w(b_off + st * B_BYTES + t * 2 * BN * 4);
+      }
       if constexpr (!G64) {
         const int sr = (k0 + 16 * t + 8 * h) / g - gi0;
         const uint32_t so = (sr * BN + colw) * 2;

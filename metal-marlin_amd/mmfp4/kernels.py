@@ -127,9 +127,9 @@ def marlin_gemm_fp4(A: torch.Tensor, B_packed: torch.Tensor, scales: torch.Tenso
 
 
 def rowpacked_gemm_supported(M: int, N: int, K: int, group_size: int) -> bool:
-    """Shapes the in-place row-packed decode kernel takes (mm_fp4_gemm_rowpacked)."""
-    return (0 < M <= 16 and K % 256 == 0 and group_size > 0 and group_size % 64 == 0
-            and K % group_size == 0 and N % 4 == 0)
+    """Shapes mm_fp4_gemm_rowpacked takes (row-packed words read in place)."""
+    return (M > 0 and K % 256 == 0 and group_size > 0 and group_size % 64 == 0
+            and K % group_size == 0 and N % (4 if M <= 16 else 8) == 0)
 
 
 def _scales_layout(scales: torch.Tensor, N: int, n_groups: int, name: str = "scales") -> int:
@@ -148,7 +148,10 @@ def mmfp4_gemm_rowpacked(A: torch.Tensor, B_rows: torch.Tensor, scales: torch.Te
                          group_size: int = 128) -> torch.Tensor:
     """A [M, K] @ dequant(B_rows)^T with row-packed weights read in place:
     B_rows [N, K/8] words, scales [K/group_size, N] (the layer's canonical
-    layout) or [N, K/group_size] (layers/mmfp4_linear.py:549-598), M <= 16."""
+    layout) or [N, K/group_size] (layers/mmfp4_linear.py:549-598).  M <= 16
+    runs the decode kernels; larger M the pipelined prefill kernel, which
+    reads the words in place too but takes [K/group_size, N] scales (the
+    other layout is transposed here, K/group_size x N halves)."""
     dev = _lib.require_device(A, B_rows, scales)
     M, K = A.shape
     N, K_packed = B_rows.shape
@@ -160,6 +163,8 @@ def mmfp4_gemm_rowpacked(A: torch.Tensor, B_rows: torch.Tensor, scales: torch.Te
     a = _half(A)
     b = _packed(B_rows)
     s = _half(scales)
+    if M > 16 and layout == 1:
+        s, layout = s.t().contiguous(), 0
     out = torch.empty((M, N), dtype=torch.float16, device=dev)
     ws = _lib.workspace(dev, int(_lib.load().mm_gemm_workspace_bytes(M, N, K)))
     _lib.call("mm_fp4_gemm_rowpacked", _lib.ptr(a), _lib.ptr(b), _lib.ptr(s), _lib.ptr(out), M, N,
@@ -257,7 +262,7 @@ def mmfp4_fused_gate_up(x: torch.Tensor, gate_packed: torch.Tensor, gate_scales:
         if tuple(sc.shape) != expected:
             raise ValueError(f"{name} shape mismatch: expected {expected}, got {tuple(sc.shape)}")
     M = x.shape[0]
-    if rowpacked_gemm_supported(M, N, K, group_size) and N % 8 == 0:
+    if M <= 16 and rowpacked_gemm_supported(M, N, K, group_size) and N % 8 == 0:
         # decode sizes: the row-packed words are read in place, no transpose
         dev = _lib.require_device(x, gate_packed, gate_scales, up_packed, up_scales)
         a = _half(x)

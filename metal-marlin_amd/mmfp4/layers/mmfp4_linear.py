@@ -3,12 +3,14 @@ mmfp4_linear.py:414-478, 549-598, 600-960).
 
 Row-packed means `packed_weights` uint32 [out_features, in_features // 8],
 word (n, j) holding inputs 8j..8j+7 of output n (LSB first); scales are
-[n_groups, out_features] or [out_features, n_groups].  At decode sizes
-(M <= 16, K % 256 == 0, group size % 64 == 0) both the functional
-`mmfp4_gemm` and `MMFP4Linear` read the row-packed words and the scales in
-place (mm_fp4_gemm_rowpacked).  Larger M runs the prefill kernels, which read
-the Marlin layout [in // 8, out]: the functional form converts per call (as
-the reference does on every call); the layer converts once on the device and
+[n_groups, out_features] or [out_features, n_groups].  When K % 256 == 0
+and the group size is a multiple of 64 (and out_features % 8 == 0 above 16
+rows), both the functional `mmfp4_gemm` and `MMFP4Linear` read the
+row-packed words in place at every M (mm_fp4_gemm_rowpacked: the decode
+kernels up to 16 rows, the pipelined prefill kernel above), so the layer
+holds one copy of its weights.  Other shapes run the Marlin-layout kernels
+on [in // 8, out] words: the functional form converts per call (as the
+reference does on every call); the layer converts once on the device and
 keeps the copy as a non-persistent buffer (the reference's
 `_kernel_packed_weights`), rebuilt whenever `packed_weights` is written or
 replaced.  The reference's M <= 16 path dequantises the whole weight to fp16
@@ -70,7 +72,7 @@ def mmfp4_gemm(x: torch.Tensor, packed_weights: torch.Tensor, scales: torch.Tens
     out_f, in_f = packed_weights.shape[0], packed_weights.shape[1] * 8
     n_groups = -(-in_f // group_size)
     if kernels.rowpacked_gemm_supported(x.shape[0], out_f, in_f, group_size):
-        # decode sizes: the row-packed words are read in place, no transpose
+        # the row-packed words are read in place, no transpose
         return kernels.mmfp4_gemm_rowpacked(x, _as_words(packed_weights), scales, group_size)
     s = _scales_groups_first(scales, out_f, n_groups)
     return kernels.marlin_gemm_fp4(x, rowpacked_to_marlin(packed_weights), s, group_size)
@@ -133,7 +135,7 @@ class MMFP4Linear(nn.Module):
         scales = self.scales.to(x.device)
         if kernels.rowpacked_gemm_supported(x2.shape[0], self.out_features, self.in_features,
                                             self.group_size):
-            # decode sizes: row-packed words and [n_groups, out] scales in place
+            # row-packed words and [n_groups, out] scales in place
             out = kernels.mmfp4_gemm_rowpacked(x2, self.packed_weights.to(x.device), scales,
                                                self.group_size)
         else:

@@ -73,13 +73,16 @@ def test_dispatch_gemm_fp4_and_gemmfp4(rng):
 @pytest.mark.parametrize("M,K,N,g", [(1, 4096, 4096, 128), (4, 14336, 4096, 128),
                                      (16, 4096, 6144, 64), (1, 256, 4, 256), (7, 1024, 100, 128),
                                      (1, 4096, 28672, 128), (3, 2048, 1028, 64),
-                                     (2, 4096, 6144, 128), (8, 1024, 3072, 64), (5, 4608, 4100, 128)])
+                                     (2, 4096, 6144, 128), (8, 1024, 3072, 64), (5, 4608, 4100, 128),
+                                     (17, 14336, 4096, 128), (40, 4096, 4096, 128),
+                                     (300, 2048, 1000, 64), (1024, 4096, 2048, 128)])
 def test_rowpacked_gemm_in_place(M, K, N, g):
     """mm_fp4_gemm_rowpacked reads [N, K/8] words and the scales in place, in
     either layout the layer accepts ([K/g, N] canonical, [N, K/g] transposed)
     (layers/mmfp4_linear.py:549-598 without its per-call transpose): parity
     with the fp32 reference of the same weights, including the split-K shape
-    14336 -> 4096.  Both scale layouts give bit-identical results."""
+    14336 -> 4096, and above 16 rows the pipelined prefill kernel on the same
+    words.  Both scale layouts give bit-identical results."""
     import mmfp4
     gen = torch.Generator(device="cuda").manual_seed(M * 3 + K + N)
     w = (torch.randn((N, K), generator=gen, device="cuda") * 0.02).half()
@@ -103,8 +106,8 @@ def test_rowpacked_gemm_refuses_unsupported_shapes():
     a = torch.zeros((17, 512), dtype=torch.float16, device="cuda")
     rows = torch.zeros((64, 64), dtype=torch.int32, device="cuda")
     s = torch.ones((64, 4), dtype=torch.float16, device="cuda")
-    with pytest.raises(ValueError):                          # M > 16
-        mmfp4.mmfp4_gemm_rowpacked(a, rows, s, 128)
+    with pytest.raises(ValueError):                          # M > 16 needs N % 8 == 0
+        mmfp4.mmfp4_gemm_rowpacked(a, rows[:60], s[:60], 128)
     with pytest.raises(ValueError):                          # K % 256 != 0
         mmfp4.mmfp4_gemm_rowpacked(a[:1, :384], rows[:, :48], s[:, :3], 128)
     with pytest.raises(ValueError):                          # group size % 64 != 0
@@ -161,12 +164,14 @@ def test_mmfp4_gemm_rejects_mismatched_scales():
         mmfp4.mmfp4_gemm(a, p, torch.ones((5, 96), dtype=torch.float16, device="cuda"), 128)
 
 
-def test_mmfp4_linear_reloaded_weights_take_effect(rng):
-    """MMFP4Linear's Marlin-layout copy (used at M > 16) follows writes to
-    packed_weights: load_state_dict with new weights changes the output at
-    every M, and matches the oracle of the new weights."""
+@pytest.mark.parametrize("g", [128, 32])
+def test_mmfp4_linear_reloaded_weights_take_effect(rng, g):
+    """load_state_dict with new weights changes MMFP4Linear's output at every
+    M and matches the oracle of the new weights: g=128 reads the row-packed
+    words in place at both sizes; g=32 (not a multiple of 64) runs the
+    Marlin-layout copy, which must follow writes to packed_weights."""
     import mmfp4
-    out_f, in_f, g = 256, 512, 128
+    out_f, in_f = 256, 512
     w1 = rng.normal(0, 0.02, (out_f, in_f)).astype(np.float16)
     w2 = rng.normal(0, 0.02, (out_f, in_f)).astype(np.float16)
     m1, s1 = ofp4.quantize_fp4(w1, g)
