@@ -136,7 +136,8 @@ int mm_fp4_gemm_mmfp4(const uint16_t* A, const uint32_t* B, const uint16_t* scal
 
 /* mm_fp4_gate_up for row-packed (MMFP4) gate and up matrices read in place:
  * Bg, Bu [N, K/8] uint32, scales Sg, Su fp16 [K/g, N]; act as mm_fp4_gate_up.
- * Decode sizes only: M <= 16, K % 256 == 0, g % 64 == 0, N % 8 == 0.
+ * K % 256 == 0, g % 64 == 0, N % 8 == 0; M <= 16 runs the decode kernel, larger
+ * M the pipelined prefill kernel, both reading the words in place.
  * Workspace: mm_gemm_workspace_bytes(M, 2N, K).  Replaces
  * metal_marlin/kernels_core.py:4762-4774 (mmfp4_fused_gate_up) ->
  * MetalKernels.mmfp4_fused_gate_up :4269-4408 on its row-packed inputs,

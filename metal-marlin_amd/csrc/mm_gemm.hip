@@ -495,7 +495,27 @@ struct PairSrc {
   }
 };
 
-// ROWS: B is row-packed [N, K/8] (SK_PLAIN only).
+// Gate/up pair over row-packed [N, K/8] words (kp = K/8 words per column).
+struct PairRowSrc {
+  static constexpr bool kRowPacked = true;
+  const f16* A;
+  int lda, M, m0, N, n0;
+  const uint32_t *B, *B2;
+  const f16 *S, *S2, *Z, *Z2;
+  int ld, kp;
+  MM_DEV const f16* arow(int r) const { return A + (size_t)min(m0 + r, M - 1) * lda; }
+  MM_DEV const uint32_t* brow(int P) const {
+    return (pair_is_up(P) ? B2 : B) + (size_t)pair_out_col(n0, P, 1, N) * kp;
+  }
+  MM_DEV const f16* scol(int P, int w) const {
+    return (pair_is_up(P) ? S2 : S) + pair_out_col(n0, P, w, N);
+  }
+  MM_DEV const f16* zcol(int P, int w) const {
+    return (pair_is_up(P) ? Z2 : Z) + pair_out_col(n0, P, w, N);
+  }
+};
+
+// ROWS: B (and B2) are row-packed [N, K/8] FP4 words.
 template <bool INT4, int WM, int WN, int RB, int CW, bool G64, int ACT, bool ROWS = false>
 __global__ void __launch_bounds__(WM * WN * 64)
 k_prefill2(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
@@ -508,7 +528,7 @@ k_prefill2(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
   // columns and tile 1 the same 32 up columns, so a block covers BN/2 output
   // columns.  Requires K % 64 == 0 and N % 8 == 0 (checked by the host).
   static_assert(ACT == SK_PLAIN || CW == 2, "pair modes pair two column tiles");
-  static_assert(!ROWS || (ACT == SK_PLAIN && !INT4), "row-packed weights: plain FP4 product");
+  static_assert(!ROWS || !INT4, "row-packed weights: FP4");
   constexpr int SROWS = G64 ? PF2_SROWS_G64 : PF2_SROWS;
   using Sh = Pf2Shape<INT4, WM, WN, RB, CW, PF2_STAGES, SROWS>;
   __shared__ __attribute__((aligned(16))) char smem[Sh::LDS_BYTES];
@@ -524,10 +544,14 @@ k_prefill2(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
   const int c_beg = blockIdx.z * cps;
   const int c_end = min(nch_all, c_beg + cps);
   f32x16 acc[RB][CW];
-  if constexpr (ROWS) {
+  if constexpr (ROWS && ACT == SK_PLAIN) {
     const DenseRowSrc src{A, lda, M, m0, N, n0, B, S, Z, N, K / 8};
     pf2_mainloop<INT4, WM, WN, RB, CW, G64, false, PF2_STAGES, SROWS>(src, K, g, c_beg, c_end,
                                                                   smem, acc);
+  } else if constexpr (ROWS) {
+    const PairRowSrc src{A, lda, M, m0, N, n0, B, B2, S, S2, Z, Z2, N, K / 8};
+    pf2_mainloop<INT4, WM, WN, RB, CW, G64, true, PF2_STAGES, SROWS>(src, K, g, c_beg, c_end,
+                                                                 smem, acc);
   } else if constexpr (ACT == SK_PLAIN) {
     const DenseSrc src{A, lda, M, m0, N, n0, B, S, Z, N};
     pf2_mainloop<INT4, WM, WN, RB, CW, G64, false, PF2_STAGES, SROWS>(src, K, g, c_beg, c_end,
@@ -1184,20 +1208,37 @@ extern "C" int mm_fp4_gate_up_rowpacked(const uint16_t* A, const uint32_t* Bg, c
   const char* who = "mm_fp4_gate_up_rowpacked";
   MM_CHECK_ARG(act == 0 || act == 1, "%s: act=%d must be 0 or 1", who, act);
   MM_CHECK_ARG(M >= 0 && N > 0 && K > 0, "%s: bad shape M=%d N=%d K=%d", who, M, N, K);
-  MM_CHECK_ARG(M <= 16, "%s: M=%d: the row-packed decode kernel takes M <= 16 (larger M: "
-               "transpose to the [K/8, N] layout and call mm_fp4_gate_up)", who, M);
   MM_CHECK_ARG(K % 256 == 0, "%s: K=%d must be divisible by 256", who, K);
   MM_CHECK_ARG(g > 0 && g % 64 == 0 && K % g == 0,
                "%s: group_size=%d must be a multiple of 64 dividing K=%d", who, g, K);
   MM_CHECK_ARG(N % 8 == 0, "%s: N=%d must be divisible by 8", who, N);
-  MM_CHECK_ARG((size_t)N * (size_t)(K / 8) * 4 < ((size_t)1 << 32),
-               "%s: each packed matrix must be under 4 GiB", who);
+  MM_CHECK_ARG(M > 16 || (size_t)N * (size_t)(K / 8) * 4 < ((size_t)1 << 32),
+               "%s: each packed matrix must be under 4 GiB at M <= 16", who);
   const uintptr_t a16 = (uintptr_t)A | (uintptr_t)Bg | (uintptr_t)Bu;
   MM_CHECK_ARG((a16 & 15) == 0 && (((uintptr_t)Sg | (uintptr_t)Su) & 7) == 0 &&
                    ((uintptr_t)C & 7) == 0,
                "%s: A and the packed weights must be 16-byte aligned, scales and C 8-byte", who);
   if (M == 0) return 0;
   const int ldc = act ? N : 2 * N;
+  if (M > 16) {
+    // Pipelined prefill kernel reading both row-packed matrices in place;
+    // split and workspace as the unfused [K, 2N] product.
+    const PrefillPlan p = plan_prefill(M, 2 * N, K);
+    float* part = nullptr;
+    if (p.ksplit > 1) {
+      const size_t need = SK_COUNTER_BYTES + prefill_ws_bytes(M, 2 * N, K);
+      MM_CHECK_ARG(ws != nullptr && ws_bytes >= need,
+                   "%s: workspace of %zu bytes is smaller than the %zu required", who, ws_bytes,
+                   need);
+      part = (float*)((char*)ws + SK_COUNTER_BYTES);
+    }
+    const f16 *a = (const f16*)A, *sg = (const f16*)Sg, *su = (const f16*)Su;
+    hipStream_t st = (hipStream_t)stream;
+#define MM_LAUNCH_ROWS_PAIR(ACTV)                                                                  switch (p.cfg) {                                                                               case 0:                                                                                        return launch_prefill2<false, ACTV, PF2_BIG, true>(a, K, Bg, sg, nullptr, Bu, su, nullptr,                                                          (f16*)C, ldc, M, N, K, g, p.ksplit,                                                            part, st);                                case 1:                                                                                        return launch_prefill2<false, ACTV, PF2_MID, true>(a, K, Bg, sg, nullptr, Bu, su, nullptr,                                                          (f16*)C, ldc, M, N, K, g, p.ksplit,                                                            part, st);                                default:                                                                                       return launch_prefill2<false, ACTV, PF2_SMALL, true>(a, K, Bg, sg, nullptr, Bu, su,                                                                 nullptr, (f16*)C, ldc, M, N, K, g,                                                             p.ksplit, part, st);                  }
+    if (act) MM_LAUNCH_ROWS_PAIR(SK_SWIGLU)
+    MM_LAUNCH_ROWS_PAIR(SK_PAIR)
+#undef MM_LAUNCH_ROWS_PAIR
+  }
   if (act)
     return launch_skinny<false, 1, SK_SWIGLU, 2>((const f16*)A, K, Bg, (const f16*)Sg, nullptr,
                                                  Bu, (const f16*)Su, nullptr, (f16*)C, ldc, M,

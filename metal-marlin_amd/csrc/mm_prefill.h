@@ -140,22 +140,23 @@ MM_DEV void pf2_mainloop(const Src& src, int K, int g, int c_beg, int c_end, cha
   }
   // Marlin-layout B: piece p is 4 columns of one word row; the stage holds
   // [8 word rows][BN columns].  Row-packed B (ROWP): piece p is 4 words (16
-  // bytes) of one column, half hf = words 4hf..4hf+3; the stage holds
-  // [CW][BN/CW][2 halves] pieces, column P = CW*c + j at slot
-  // 2*(j*(BN/CW) + c) + hf.  A load instruction then reads both halves (32
-  // contiguous bytes) of 32 columns, and the 16 lanes of an LDS read pass
-  // read every other piece of a 512-byte span.  Both layouts are loaded
-  // global -> LDS directly.
+  // bytes) of one column, half hf = words 4hf..4hf+3, at slot 2*q + hf, where
+  // q orders the columns as the lanes read them: q = P for the tile-major
+  // read (column tile j of a wave is 32 consecutive columns); otherwise, with
+  // column P = CW*c + j, q = j*(BN/CW) + c.  A load instruction then reads
+  // both halves (32 contiguous bytes) of 32 columns, and the 16 lanes of an
+  // LDS read pass read every other piece of a 512-byte span.  Both layouts
+  // are loaded global -> LDS directly.
   constexpr bool ROWP = is_rowpacked<Src>::value;
-  static_assert(!ROWP || (G64 && !TM), "row-packed B: one group per chunk, adjacent columns");
+  static_assert(!ROWP || G64, "row-packed B: one group per chunk");
   const uint32_t* b_src[B_IT];
 #pragma unroll
   for (int i = 0; i < B_IT; ++i) {
     const int p = min((i * NWAVE + wave) * 64 + lane, Sh::B_PIECES - 1);
     if constexpr (ROWP) {
-      const int hf = p % 2, rem = p / 2;     // B_PIECES == 2 * BN
-      const int j = rem / (BN / CW), c = rem % (BN / CW);
-      b_src[i] = src.brow(c * CW + j) + 4 * hf;
+      const int hf = p % 2, q = p / 2;       // B_PIECES == 2 * BN
+      const int P = TM ? q : (q % (BN / CW)) * CW + q / (BN / CW);
+      b_src[i] = src.brow(P) + 4 * hf;
     } else {
       b_src[i] = src.bcol(4 * (p % (BN / 4)), 4) + (size_t)(p / (BN / 4)) * ld;
     }
@@ -219,9 +220,10 @@ MM_DEV void pf2_mainloop(const Src& src, int K, int g, int c_beg, int c_end, cha
   for (int t = 0; t < PF2_BK / 16; ++t)
     a_off[t] = ROWP ? arow * 128 + ((4 * h + t) ^ ((arow >> 1) & 7)) * 16
                     : arow * 128 + ((2 * t) ^ hx) * 16;
-  // + st*B_BYTES, and + t*2*BN*4 (Marlin) or + j*(BN/CW)*32 (ROWP)
-  const uint32_t b_off = ROWP ? B_OFF + ((wn * 32 + l32) * 2 + h) * 16
+  // + st*B_BYTES, and + t*2*BN*4 (Marlin) or + j*BSTEP (ROWP)
+  const uint32_t b_off = ROWP ? B_OFF + ((TM ? colw : wn * 32 + l32) * 2 + h) * 16
                               : B_OFF + (h * BN + colw) * 4;
+  constexpr int BSTEP = TM ? 32 * 32 : (BN / CW) * 32;
   typedef uint32_t wvec __attribute__((ext_vector_type(CW)));
   typedef f16 svec __attribute__((ext_vector_type(CW)));
   auto read_w = [&](uint32_t off) {
@@ -266,7 +268,7 @@ MM_DEV void pf2_mainloop(const Src& src, int K, int g, int c_beg, int c_end, cha
     if constexpr (ROWP) {
 #pragma unroll
       for (int j = 0; j < CW; ++j)
-        bp[j] = *(const u32x4*)(smem + b_off + st * B_BYTES + j * (BN / CW) * 32);
+        bp[j] = *(const u32x4*)(smem + b_off + st * B_BYTES + j * BSTEP);
     }
     if constexpr (G64) {
       const svec s0 = read_s(S_OFF + st * S_BYTES + colw * 2);

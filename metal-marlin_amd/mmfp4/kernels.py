@@ -239,11 +239,12 @@ def mmfp4_fused_gate_up(x: torch.Tensor, gate_packed: torch.Tensor, gate_scales:
     """silu(gate_proj(x)) * up_proj(x) (kernels_core.py:4762-4774 ->
     MetalKernels.mmfp4_fused_gate_up :4269-4408).  Layout as documented there:
     gate_packed / up_packed row-packed [N, K/8] uint32, scales [K/group_size, N].
-    At decode sizes (M <= 16, K % 256 == 0, group size % 64 == 0) the
-    row-packed words are read in place (mm_fp4_gate_up_rowpacked); otherwise
-    they are transposed to the Marlin layout on the device for each call (as
-    the reference's own M < 64 path does); callers that keep the Marlin layout
-    call `mmfp4_fused_gate_up_marlin` and skip the transpose.
+    With K % 256 == 0, group size % 64 == 0 and N % 8 == 0 the row-packed
+    words are read in place at every M (mm_fp4_gate_up_rowpacked: the decode
+    kernel up to 16 rows, the pipelined prefill kernel above); other shapes
+    are transposed to the Marlin layout on the device for each call (as the
+    reference's own M < 64 path does); callers that keep the Marlin layout
+    call `mmfp4_fused_gate_up_marlin`.
     SiLU is applied to the fp32 sums (the reference rounds them to fp16 first)."""
     if x.dim() != 2:
         raise ValueError(f"x must be 2D [M, K], got shape={tuple(x.shape)}")
@@ -262,8 +263,8 @@ def mmfp4_fused_gate_up(x: torch.Tensor, gate_packed: torch.Tensor, gate_scales:
         if tuple(sc.shape) != expected:
             raise ValueError(f"{name} shape mismatch: expected {expected}, got {tuple(sc.shape)}")
     M = x.shape[0]
-    if M <= 16 and rowpacked_gemm_supported(M, N, K, group_size) and N % 8 == 0:
-        # decode sizes: the row-packed words are read in place, no transpose
+    if rowpacked_gemm_supported(M, N, K, group_size) and N % 8 == 0:
+        # the row-packed words are read in place, no transpose
         dev = _lib.require_device(x, gate_packed, gate_scales, up_packed, up_scales)
         a = _half(x)
         out = torch.empty((M, N), dtype=torch.float16, device=dev)

@@ -142,9 +142,10 @@ def test_multi_qkv_bit_exact(rng, M):
         _same(o, ofp4.gemm_fp4_ref(a, p, s, g))
 
 
-@pytest.mark.parametrize("M", [1, 24, 256])
+@pytest.mark.parametrize("M", [1, 24, 256, 2048])
 def test_gate_up_pair_bit_exact(rng, M):
-    """Pair mode without the SwiGLU (act=0): [x @ Wg | x @ Wu]."""
+    """Pair mode without the SwiGLU (act=0): [x @ Wg | x @ Wu], on Marlin
+    and on row-packed words."""
     import mmfp4
     K, N, g = 4096, 3072, 128
     gp, gs = _exact_fp4(rng, K, N, g)
@@ -154,6 +155,17 @@ def test_gate_up_pair_bit_exact(rng, M):
     announce(f"exact gate/up pair M={M}")
     _same(mmfp4.fused_gate_up_gemm(to_dev(a), to_dev(gp), to_dev(gs), to_dev(up), to_dev(us), g),
           ref)
+    # the same pair on row-packed words, read in place (act=0 through the C ABI)
+    from mmfp4 import _lib
+    da = to_dev(a)
+    rg, ru = to_dev(np.ascontiguousarray(gp.T)), to_dev(np.ascontiguousarray(up.T))
+    dgs, dus = to_dev(gs), to_dev(us)
+    out = torch.empty((M, 2 * N), dtype=torch.float16, device="cuda")
+    ws = _lib.workspace(out.device, int(_lib.load().mm_gemm_workspace_bytes(M, 2 * N, K)))
+    _lib.call("mm_fp4_gate_up_rowpacked", _lib.ptr(da), _lib.ptr(rg), _lib.ptr(dgs),
+              _lib.ptr(ru), _lib.ptr(dus), _lib.ptr(out), M, N, K, g, 0, _lib.ptr(ws),
+              ws.numel(), _lib.stream_of(da))
+    _same(out, ref)
 
 
 @pytest.mark.parametrize("T,k,E,K,N", [(32, 8, 128, 2048, 1536), (32, 8, 128, 768, 2048),
