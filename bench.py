@@ -303,20 +303,26 @@ def run_fused_bench(torch, mmfp4, steps: int):
             "fused_TBps": round(byts / (uf * 1e-6) / 1e12, 3),
             "fused_TFLOPs": round(4 * M * K * N / (uf * 1e-6) / 1e12, 1),
             "unfused": "marlin_gemm_fp4 on the concatenated [K/8, 2N] weights + torch silu*mul"}
-    # The reference's mmfp4_fused_gate_up takes row-packed [N, K/8] weights: read in place
-    # (decode sizes) against transposing them per call, as the reference does.
+    # The reference's mmfp4_fused_gate_up and MMFP4 GEMM take row-packed [N, K/8] weights:
+    # read in place against transposing them per call, as the reference does.
     rows = [((g[0].t().contiguous(), g[1]), (u[0].t().contiguous(), u[1])) for g, u in gu]
     del cat
-    a = torch.randn((1, K), generator=gen, device="cuda").half()
-    inplace = [[lambda w=w: mmfp4.mmfp4_fused_gate_up(a, w[0][0], w[0][1], w[1][0], w[1][1], G)]
-               for w in rows]
-    transp = [[lambda w=w: mmfp4.mmfp4_fused_gate_up_marlin(
-        a, w[0][0].t().contiguous(), w[0][1], w[1][0].t().contiguous(), w[1][1], G)] for w in rows]
-    ui = 1e3 * timed_launches(torch, inplace, steps, 5) / steps
-    ut = 1e3 * timed_launches(torch, transp, max(5, steps // 4), 3) / max(5, steps // 4)
-    res["gate_up_silu_rowpacked_M1"] = {
-        "K": K, "N_each": N, "in_place_us": round(ui, 2), "transpose_per_call_us": round(ut, 2),
-        "in_place_TBps": round((2 * alg_bytes(1, K, N) - 2 * K) / (ui * 1e-6) / 1e12, 3)}
+    for M, st in ((1, steps), (2048, max(3, steps // 40))):
+        a = torch.randn((M, K), generator=gen, device="cuda").half()
+        inplace = [[lambda w=w: mmfp4.mmfp4_fused_gate_up(a, w[0][0], w[0][1], w[1][0], w[1][1],
+                                                          G)] for w in rows]
+        transp = [[lambda w=w: mmfp4.mmfp4_fused_gate_up_marlin(
+            a, w[0][0].t().contiguous(), w[0][1], w[1][0].t().contiguous(), w[1][1], G)]
+            for w in rows]
+        one = [[lambda w=w: mmfp4.mmfp4_gemm_rowpacked(a, w[0][0], w[0][1], G)] for w in rows]
+        ui = 1e3 * timed_launches(torch, inplace, st, 3) / st
+        ut = 1e3 * timed_launches(torch, transp, max(3, st // 4), 2) / max(3, st // 4)
+        uo = 1e3 * timed_launches(torch, one, st, 3) / st
+        res[f"rowpacked_M{M}"] = {
+            "K": K, "N": N, "gate_up_silu_in_place_us": round(ui, 2),
+            "gate_up_silu_transpose_per_call_us": round(ut, 2),
+            "gemm_in_place_us": round(uo, 2),
+            "gate_up_silu_in_place_TFLOPs": round(4 * M * K * N / (ui * 1e-6) / 1e12, 1)}
     del gu, rows
     Ns = (4096, 1024, 1024)
     copies = max(2, -(-ROTATE_BYTES // sum(alg_bytes(0, K, n) for n in Ns)))
