@@ -70,3 +70,40 @@ def test_fuzz_gate_up(M, K, N, g):
     announce(f"fuzz gate_up M={M} K={K} N={N} g={g}")
     out = mmfp4.mmfp4_fused_gate_up_marlin(a, gp, gs, up, us, g)
     assert max_abs_rel(to_np(out), to_np(torch.nn.functional.silu(hg) * hu)) <= TOL
+
+
+def _rowpacked_shapes(seed, n):
+    r = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        g = int(r.choice([64, 128, 256]))
+        K = 256 * int(r.integers(1, 17))
+        if K % g:
+            continue
+        N = 8 * int(r.integers(1, 700))
+        M = int(r.choice([1, 5, 16, 17, 31, 33, 64, 100, 257, 600]))
+        out.append((M, K, N, g))
+    return out
+
+
+@pytest.mark.parametrize("M,K,N,g", _rowpacked_shapes(321, 16))
+def test_fuzz_rowpacked(M, K, N, g):
+    """Row-packed [N, K/8] words read in place (decode and prefill kernels),
+    the plain product and the gate/up pair, both scale layouts."""
+    import mmfp4
+    gen = torch.Generator(device="cuda").manual_seed(M * 7 + K * 3 + N)
+    wg = (torch.randn((N, K), generator=gen, device="cuda") * 0.02).half()
+    wu = (torch.randn((N, K), generator=gen, device="cuda") * 0.02).half()
+    a = torch.randn((M, K), generator=gen, device="cuda").half()
+    gp, gs = mmfp4.quantize_fp4(wg, group_size=g)
+    up, us = mmfp4.quantize_fp4(wu, group_size=g)
+    hg = a.float() @ mmfp4.dequant_fp4(gp, gs, K, N, g).float()
+    hu = a.float() @ mmfp4.dequant_fp4(up, us, K, N, g).float()
+    rg, ru = gp.t().contiguous(), up.t().contiguous()
+    announce(f"fuzz row-packed M={M} K={K} N={N} g={g}")
+    out = mmfp4.mmfp4_gemm_rowpacked(a, rg, gs, g)
+    assert max_abs_rel(to_np(out), to_np(hg)) <= TOL
+    out_t = mmfp4.mmfp4_gemm_rowpacked(a, rg, gs.t().contiguous(), g)
+    assert torch.equal(out_t.view(torch.int16), out.view(torch.int16))
+    pair = mmfp4.mmfp4_fused_gate_up(a, rg, gs, ru, us, g)
+    assert max_abs_rel(to_np(pair), to_np(torch.nn.functional.silu(hg) * hu)) <= TOL
