@@ -262,7 +262,45 @@ def run_host_paced(torch, mmfp4, n: int = 400):
         t2 = time.perf_counter()
         out[name] = {"host_enqueue_us_per_call": round(1e6 * (t1 - t0) / n, 2),
                      "wall_us_per_call": round(1e6 * (t2 - t0) / n, 2)}
+    out["llama_layer_M1"] = run_layer_graph(torch, mmfp4, max(50, n // 4))
     return out
+
+
+def run_layer_graph(torch, mmfp4, n: int):
+    """The four Llama-layer GEMMs at M=1 host-paced, eager (four library calls
+    per step) and as one captured HIP graph replayed per step: wall µs per
+    step over n back-to-back steps (same weights every step)."""
+    ws = [make_weights(torch, mmfp4, K, N, 820 + i) for i, (_, K, N) in enumerate(LLAMA_LAYER)]
+    xs = {K: torch.randn((1, K), device="cuda").half() for _, K, _ in LLAMA_LAYER}
+
+    def step():
+        return [mmfp4.marlin_gemm_fp4(xs[K], w[0], w[1], G)
+                for (_, K, _), w in zip(LLAMA_LAYER, ws)]
+
+    def wall(fn):
+        for _ in range(10):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            fn()
+        torch.cuda.synchronize()
+        return 1e6 * (time.perf_counter() - t0) / n
+
+    eager = wall(step)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()
+        step()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        step()
+    graph = wall(g.replay)
+    return {"eager_wall_us_per_step": round(eager, 2), "graph_wall_us_per_step": round(graph, 2),
+            "launches_per_step": len(LLAMA_LAYER)}
 
 
 def cpu_model_name() -> str:
