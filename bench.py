@@ -171,6 +171,14 @@ def run_prefill_bench(torch, mmfp4, M: int, steps: int, warmup: int):
             "launch_us_avg": 1e3 * total_ms / (steps * len(PREFILL))}
 
 
+def prefill_steps(args) -> tuple[int, int]:
+    """(timed, warm-up) steps of the M=2048 prefill pair.  Each step is about
+    0.5 ms of full-chip MFMA load; the clock needs ~10 ms of it to settle (a
+    measured ramp on MI355X: 851 -> 930 -> 969 -> 996 TF/s over the first
+    runs), so the untimed warm-up covers that before the timed steps."""
+    return max(20, args.steps // 5), max(20, args.warmup)
+
+
 def run_mfma_ceiling(torch, mmfp4, prefill_tflops: float):
     """The sustained MFMA 32x32x16 f16 rate on this GPU with nothing else in
     the loop (`mm_mfma_ceiling`), fed (a) the prefill GEMM's own operand
@@ -592,8 +600,7 @@ def main() -> int:
             res = {"us_per_step": round(1e3 * r["ms_per_step"], 3), "per_shape": r["per_shape"],
                    "TBps": round(r["step_bytes"] / (r["ms_per_step"] * 1e-3) / 1e12, 4)}
         elif args.section == "prefill":
-            r = run_prefill_bench(torch, mmfp4, 2048, max(5, args.steps // 20),
-                                  max(2, args.warmup // 10))
+            r = run_prefill_bench(torch, mmfp4, 2048, *prefill_steps(args))
             tf = r["flops"] / (r["ms_per_step"] * 1e-3) / 1e12
             res = {"ms_per_step": round(r["ms_per_step"], 4), "per_shape": r["per_shape"],
                    "TFLOPs": round(tf, 1), "mfma_ceiling": run_mfma_ceiling(torch, mmfp4, tf)}
@@ -602,7 +609,7 @@ def main() -> int:
         print(json.dumps({"section": args.section, "result": res}))
         return 0
     layer = run_layer_bench(torch, mmfp4, 1, args.steps, args.warmup)
-    pre = run_prefill_bench(torch, mmfp4, 2048, max(5, args.steps // 20), max(2, args.warmup // 10))
+    pre = run_prefill_bench(torch, mmfp4, 2048, *prefill_steps(args))
     value_tbs = layer["step_bytes"] / (layer["ms_per_step"] * 1e-3) / 1e12
     achieved = layer["step_bytes"] / 4 / (layer["launch_us_avg"] * 1e-6) / 1e9
     tflops = pre["flops"] / (pre["ms_per_step"] * 1e-3) / 1e12
