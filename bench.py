@@ -426,11 +426,12 @@ def hipblaslt_fp16_reference(torch, M: int):
 MOE = {"E": 128, "H": 2048, "I": 768, "k": 8}
 
 
-def run_moe_bench(torch, mmfp4, T: int, steps: int):
+def run_moe_bench(torch, mmfp4, T: int, steps: int, warmup: int = 60):
     """Qwen3-30B-A3B routed experts (config 5): sort -> gate_up (+SwiGLU) ->
     down -> combine, four launches, all 128 experts resident; router logits
     N(0,1) seed 2, fp32 softmax -> top-8 -> renormalise.  Two copies of the
-    expert weights (622 MB) are rotated so each step reads HBM."""
+    expert weights (622 MB) are rotated so each step reads HBM.  The untimed
+    warm-up (60 steps, ~10 ms at T=1024) lets the clock settle first."""
     E, H, I, k = MOE["E"], MOE["H"], MOE["I"], MOE["k"]
     sets = []
     for c in range(2):
@@ -454,7 +455,7 @@ def run_moe_bench(torch, mmfp4, T: int, steps: int):
     used = int(torch.unique(ids).numel())
     launches = [[lambda s=s: mmfp4.moe_mlp_fp4(x, s[0], s[1], s[2], s[3], ids, topw, G)]
                 for s in sets]
-    ms = timed_launches(torch, launches, steps, 4)
+    ms = timed_launches(torch, launches, steps, warmup)
     us = 1e3 * ms / steps
     per_expert = (H * 2 * I // 2 + 2 * 2 * I * (H // G)) + (I * H // 2 + 2 * H * (I // G))
     byts = used * per_expert + 2 * T * H * 2 + 2 * (T * k) * I * 2
