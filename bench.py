@@ -572,7 +572,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--all", action="store_true", help="accepted for compatibility; every "
                     "BASELINE config is reported by default")
-    ap.add_argument("--section", choices=("all", "layer", "prefill", "moe"), default="all",
+    ap.add_argument("--section", choices=("all", "layer", "prefill", "moe", "fused"),
+                    default="all",
                     help="run one workload alone (for profiling); the default runs all and "
                          "prints the contract line")
     ap.add_argument("--pmc-probe", action="store_true",
@@ -605,8 +606,10 @@ def main() -> int:
             tf = r["flops"] / (r["ms_per_step"] * 1e-3) / 1e12
             res = {"ms_per_step": round(r["ms_per_step"], 4), "per_shape": r["per_shape"],
                    "TFLOPs": round(tf, 1), "mfma_ceiling": run_mfma_ceiling(torch, mmfp4, tf)}
-        else:
+        elif args.section == "moe":
             res = [run_moe_bench(torch, mmfp4, T, 20) for T in (32, 1024)]
+        else:
+            res = run_fused_bench(torch, mmfp4, 100)
         print(json.dumps({"section": args.section, "result": res}))
         return 0
     layer = run_layer_bench(torch, mmfp4, 1, args.steps, args.warmup)
