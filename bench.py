@@ -312,14 +312,24 @@ def run_layer_graph(torch, mmfp4, n: int):
 
 
 def cpu_model_name() -> str:
-    """The host CPU's model name (what lscpu prints), from /proc/cpuinfo."""
+    """The host CPU's model name as lscpu prints it (from /proc/cpuinfo), with
+    the CPU family and model numbers, which identify the generation where a
+    virtual machine reports only a generic name (family 26 = Zen 5)."""
+    info = {}
     try:
         for line in Path("/proc/cpuinfo").read_text().splitlines():
-            if line.lower().startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            key, _, val = line.partition(":")
+            key = key.strip().lower()
+            if key in ("model name", "cpu family", "model") and key not in info:
+                info[key] = val.strip()
+            if not line.strip() and info:
+                break
     except OSError:
         pass
-    return platform.processor() or "unknown"
+    name = info.get("model name") or platform.processor() or "unknown"
+    if "cpu family" in info:
+        name += f" (family {info['cpu family']} model {info.get('model', '?')})"
+    return name
 
 
 def run_fused_bench(torch, mmfp4, steps: int):
