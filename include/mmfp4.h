@@ -166,7 +166,10 @@ int mm_fp4_gemm_multi(const uint16_t* A, int nmat, const uint32_t* const* B,
  * (flat index t*k+slot, ascending within an expert) and inverse int32 [T*k].
  * Replaces metal_marlin/moe_dispatch.py:493-555 (group_tokens_by_expert),
  * :726-786 (group_tokens_by_expert_full) and the Metal moe_gpu_sort
- * (src/moe_dispatch.metal:1600-1626).  Requires E <= 1024. */
+ * (src/moe_dispatch.metal:1600-1626).  Requires E <= 1024.  Ids outside
+ * [0, E) (the reference requires them in range) are dropped: they are placed
+ * after all experts' rows, in index order, so sorted_idx and inverse remain
+ * permutations of the T*k assignments, and offsets[E] counts the valid ones. */
 int mm_moe_sort(const int32_t* expert_ids, int T, int k, int E, int32_t* offsets,
                 int32_t* sorted_idx, int32_t* inverse, void* stream);
 
@@ -217,7 +220,8 @@ int mm_moe_grouped_gemm(const uint16_t* X, const int32_t* sorted_idx, const int3
 /* out[t, :] = sum_{j<k} probs[t, j] * Y[inverse[t*k + j], :] in fp32 (fixed
  * slot order, deterministic), written as fp16 [T, H].  Replaces
  * metal_marlin/moe_dispatch.py:812-925 (scatter_expert_outputs /
- * _aggregate_expert_outputs). */
+ * _aggregate_expert_outputs).  Every slot is read, including those of
+ * dropped ids (their Y rows are whatever the caller wrote there). */
 int mm_moe_combine(const uint16_t* Y, const float* probs, const int32_t* inverse, int T, int k,
                    int H, uint16_t* out, void* stream);
 
@@ -255,6 +259,22 @@ int mm_moe_mlp_shared_fp4(const uint16_t* X, const void* expert_ids, int ids_i64
                           const uint32_t* Bsdn, const uint16_t* Ssdn, float shared_weight,
                           const uint16_t* base, int group_size, uint16_t* act_buf,
                           uint16_t* y_buf, int32_t* sort_buf, uint16_t* out, void* stream);
+
+/* Shared + routed aggregation of one FP4 projection (no MLP):
+ *   out[t] = X[t] . W_sh + sum_j probs[t, j] * (X[t] . W_routed[e(t, j)])
+ * W_sh [K/8, N] packed (scales Ssh [K/g, N]); W_routed [E, K/8, N] (scales
+ * [E, K/g, N]); expert_ids [T, k] int32 (ids_i64 = 0) or int64 (ids_i64 = 1),
+ * probs fp32 [T, k]; fp32 sums in slot order, fp16 out [T, N].  Ids outside
+ * [0, E) contribute nothing.  N % 8 == 0.  Scratch: y_buf fp16 [T*(k+1), N],
+ * sort_buf int32 [E + 2 + 2*T*(k+1)].  Three launches (sort, one grouped
+ * launch over the routed and shared groups, combine).  Replaces
+ * metal_marlin/kernels/moe.py:182-329 (moe_shared_expert_fused_fp4, kernel
+ * src/moe_shared_expert.metal:604-). */
+int mm_moe_gemm_shared_fp4(const uint16_t* X, const void* expert_ids, int ids_i64,
+                           const float* probs, int T, int k, int E, int K, int N,
+                           const uint32_t* Bsh, const uint16_t* Ssh, const uint32_t* B,
+                           const uint16_t* S, int group_size, uint16_t* y_buf, int32_t* sort_buf,
+                           uint16_t* out, void* stream);
 
 /* ------------------------------------------- flat-group FP4 (FP4Metal) */
 

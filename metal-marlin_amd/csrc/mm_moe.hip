@@ -61,6 +61,10 @@ constexpr int SORT_KC = 8;          // 64-key chunks fetched together per wave
 // expert offsets and each wave's first position per expert; pass 2 places
 // every assignment at its wave's running position plus its rank among the
 // equal lanes below it.  Dynamic LDS: wpos[SORT_WAVES][E] ints.
+// Ids outside [0, E) (the reference requires them in range) are dropped:
+// they are placed after every expert's rows, in index order, so sorted_idx
+// and inverse stay permutations of the T*k assignments and offsets[E] counts
+// the valid ones only; no grouped GEMM reads the dropped rows.
 // SH: every token has one more slot (index kin of kin + 1) whose key is the
 // shared-expert group E - 1; n = T * (kin + 1) then, and flat indices run
 // over the kin + 1 slots.
@@ -70,6 +74,8 @@ k_moe_sort(const IdT* __restrict__ ids, int n, int E, int kin, int32_t* __restri
            int32_t* __restrict__ sorted_idx, int32_t* __restrict__ inverse) {
   extern __shared__ int wpos[];
   __shared__ int wsum[SORT_WAVES];
+  __shared__ int winv[SORT_WAVES];    // dropped (out-of-range) ids per wave
+  __shared__ int s_valid;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nbits = E > 1 ? 32 - __clz(E - 1) : 0;
   const int per = mm_cdiv(mm_cdiv(n, 64), SORT_WAVES) * 64;
@@ -78,19 +84,22 @@ k_moe_sort(const IdT* __restrict__ ids, int n, int E, int kin, int32_t* __restri
   int* mine = wpos + wave * E;
 
   for (int x = tid; x < SORT_WAVES * E; x += SORT_THREADS) wpos[x] = 0;
+  int ninv = 0;                       // this wave's dropped ids (wave-uniform)
   __syncthreads();
 
   // Keys past the segment read a clamped index (the load is unconditional, so
-  // the SORT_KC loads of a batch stay in flight together) and become -1.
+  // the SORT_KC loads of a batch stay in flight together) and become -2; an
+  // out-of-range id inside the segment becomes -1.
   auto key_at = [&](int i) {
     if constexpr (SH) {
       const int t = i / (kin + 1), j = i - t * (kin + 1);
-      if (j == kin) return i < seg1 ? E - 1 : -1;
+      if (i >= seg1) return -2;
+      if (j == kin) return E - 1;
       const long long v = (long long)ids[min(t * kin + j, n / (kin + 1) * kin - 1)];
-      return (i < seg1 && v >= 0 && v < E - 1) ? (int)v : -1;
+      return (v >= 0 && v < E - 1) ? (int)v : -1;
     } else {
       const long long v = (long long)ids[min(i, n - 1)];
-      return (i < seg1 && v >= 0 && v < E) ? (int)v : -1;
+      return i >= seg1 ? -2 : ((v >= 0 && v < E) ? (int)v : -1);
     }
   };
   auto match = [&](int key) {
@@ -110,7 +119,7 @@ k_moe_sort(const IdT* __restrict__ ids, int n, int E, int kin, int32_t* __restri
   const bool single = seg1 - seg0 <= 64 * SORT_KC;
   int skey[SORT_KC], srank[SORT_KC], sgrp[SORT_KC];
 #pragma unroll
-  for (int c = 0; c < SORT_KC; ++c) skey[c] = -1, srank[c] = 0, sgrp[c] = 0;   // empty segment
+  for (int c = 0; c < SORT_KC; ++c) skey[c] = -2, srank[c] = 0, sgrp[c] = 0;   // empty segment
   for (int s0 = seg0; s0 < seg1; s0 += 64 * SORT_KC) {       // pass 1: counts
 #pragma unroll
     for (int c = 0; c < SORT_KC; ++c) skey[c] = key_at(s0 + 64 * c + lane);
@@ -121,8 +130,10 @@ k_moe_sort(const IdT* __restrict__ ids, int n, int E, int kin, int32_t* __restri
       srank[c] = __popcll(same & below);
       sgrp[c] = (e >= 0 && srank[c] == 0) ? __popcll(same) : 0;   // set on the group's leader
       if (sgrp[c]) mine[e] += sgrp[c];
+      ninv += __popcll(__ballot(e == -1));
     }
   }
+  if (lane == 0) winv[wave] = ninv;
   __syncthreads();
 
   // Expert totals -> exclusive offsets (wave scans, then a scan of the wave
@@ -149,8 +160,23 @@ k_moe_sort(const IdT* __restrict__ ids, int n, int E, int kin, int32_t* __restri
       run += c;
     }
   }
-  if (tid == SORT_THREADS - 1) offsets[E] = wbase + incl;
+  if (tid == SORT_THREADS - 1) {
+    offsets[E] = wbase + incl;
+    s_valid = wbase + incl;
+  }
   __syncthreads();
+  // Dropped ids: this wave's first position after all valid assignments.
+  int tail = s_valid;
+  for (int w = 0; w < wave; ++w) tail += winv[w];
+  auto place_dropped = [&](int e, int i) {
+    const uint64_t m = __ballot(e == -1);
+    if (e == -1) {
+      const int pos = tail + __popcll(m & below);
+      sorted_idx[pos] = i;
+      inverse[i] = pos;
+    }
+    tail += __popcll(m);
+  };
 
   // Pass 2: placement.  Every lane reads its group's running position before
   // the leader advances it past the group (LDS ops of a wave complete in
@@ -159,13 +185,14 @@ k_moe_sort(const IdT* __restrict__ ids, int n, int E, int kin, int32_t* __restri
 #pragma unroll
     for (int c = 0; c < SORT_KC; ++c) {
       const int e = skey[c];
+      const int i = seg0 + 64 * c + lane;
       if (e >= 0) {
-        const int i = seg0 + 64 * c + lane;
         const int pos = mine[e] + srank[c];
         sorted_idx[pos] = i;
         inverse[i] = pos;
       }
       if (sgrp[c]) mine[e] += sgrp[c];
+      place_dropped(e, i);
     }
     return;
   }
@@ -183,6 +210,7 @@ k_moe_sort(const IdT* __restrict__ ids, int n, int E, int kin, int32_t* __restri
         inverse[i] = pos;
       }
       if (e >= 0 && (same & below) == 0) mine[e] += __popcll(same);
+      place_dropped(e, i);
     }
   }
 }
@@ -403,12 +431,15 @@ k_moe_prefill(const f16* __restrict__ X, const int32_t* __restrict__ sorted_idx,
 // probs[t, j] for the kin routed slots and p_kin = wsh for the shared slot
 // (k = kin + 1 when a shared expert ran as an extra group, else k = kin);
 // base may be null.  Summed in fp32 in slot order; one block per token, 8
-// columns per thread.
+// columns per thread.  nvalid (may be null): the sort's count of valid
+// assignments; slots placed at or past it (dropped ids) contribute nothing.
 __global__ void __launch_bounds__(256)
 k_moe_combine(const f16* __restrict__ Y, const float* __restrict__ probs,
               const int32_t* __restrict__ inverse, int k, int kin, float wsh,
-              const f16* __restrict__ base, int H, f16* __restrict__ out) {
+              const f16* __restrict__ base, const int32_t* __restrict__ nvalid, int H,
+              f16* __restrict__ out) {
   const int t = blockIdx.x;
+  const int lim = nvalid ? *nvalid : 0x7fffffff;
   for (int h8 = threadIdx.x; h8 < H / 8; h8 += 256) {
     float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     if (base) {
@@ -418,7 +449,9 @@ k_moe_combine(const f16* __restrict__ Y, const float* __restrict__ probs,
     }
     for (int j = 0; j < k; ++j) {
       const float p = j < kin ? probs[(size_t)t * kin + j] : wsh;
-      const f16x8 y = *(const f16x8*)(Y + (size_t)inverse[(size_t)t * k + j] * H + 8 * h8);
+      const int r = inverse[(size_t)t * k + j];
+      if (r >= lim) continue;
+      const f16x8 y = *(const f16x8*)(Y + (size_t)r * H + 8 * h8);
 #pragma unroll
       for (int i = 0; i < 8; ++i) acc[i] += p * (float)y[i];
     }
@@ -533,12 +566,13 @@ int grouped_gemm(const uint16_t* X, const int32_t* sorted_idx, const int32_t* of
 
 
 int combine(const uint16_t* Y, const float* probs, const int32_t* inverse, int T, int k, int kin,
-            float wsh, const uint16_t* base, int H, uint16_t* out, void* stream) {
+            float wsh, const uint16_t* base, const int32_t* nvalid, int H, uint16_t* out,
+            void* stream) {
   MM_CHECK_ARG(T >= 0 && k > 0 && H > 0, "mm_moe_combine: bad shape");
   MM_CHECK_ARG(H % 8 == 0, "mm_moe_combine: H=%d must be divisible by 8", H);
   if (T == 0) return 0;
   hipLaunchKernelGGL(k_moe_combine, dim3(T), dim3(256), 0, (hipStream_t)stream, (const f16*)Y,
-                     probs, inverse, k, kin, wsh, (const f16*)base, H, (f16*)out);
+                     probs, inverse, k, kin, wsh, (const f16*)base, nvalid, H, (f16*)out);
   MM_CHECK_LAUNCH("mm_moe_combine");
   return 0;
 }
@@ -581,7 +615,36 @@ int moe_mlp(const char* who, const uint16_t* X, const IdT* ids, const float* pro
   if (rc) return rc;
   rc = grouped_gemm(act_buf, sorted_idx, offsets, 0, kt, T, wdn, G, I, H, g, 0, y_buf, stream);
   if (rc) return rc;
-  return combine(y_buf, probs, inverse, T, kt, k, wsh, base, H, out, stream);
+  return combine(y_buf, probs, inverse, T, kt, k, wsh, base, offsets + G, H, out, stream);
+}
+
+// Shared + routed aggregation of one FP4 projection (no MLP): every token
+// runs the shared matrix with weight 1 and its k routed matrices with their
+// probabilities, all as groups of one grouped launch (act = 0), then the
+// combine.  y_buf [T*(k+1), N] fp16, sort_buf [E + 2 + 2*T*(k+1)] int32.
+template <typename IdT>
+int moe_gemm_shared(const char* who, const uint16_t* X, const IdT* ids, const float* probs,
+                    int T, int k, int E, int K, int N, const uint32_t* Bsh, const uint16_t* Ssh,
+                    const uint32_t* B, const uint16_t* S, int g, uint16_t* y_buf,
+                    int32_t* sort_buf, uint16_t* out, void* stream) {
+  MM_CHECK_ARG(T >= 0 && k >= 0 && E >= 0 && K > 0 && N > 0 && (E > 0 || k == 0),
+               "%s: bad shape", who);
+  MM_CHECK_ARG(Bsh != nullptr && Ssh != nullptr, "%s: the shared matrix is required", who);
+  MM_CHECK_ARG(N % 8 == 0, "%s: N=%d must be divisible by 8", who, N);
+  if (T == 0) return 0;
+  MM_CHECK_ARG(y_buf != nullptr && sort_buf != nullptr && out != nullptr,
+               "%s: scratch and output buffers are required", who);
+  const int G = E + 1, kt = k + 1;
+  const long tk = (long)T * kt;
+  int32_t* offsets = sort_buf;
+  int32_t* sorted_idx = sort_buf + G + 1;
+  int32_t* inverse = sorted_idx + tk;
+  int rc = moe_sort(who, ids, T, k, G, offsets, sorted_idx, inverse, stream, true);
+  if (rc) return rc;
+  const ExpertW w{B, (const f16*)S, Bsh, (const f16*)Ssh, E};
+  rc = grouped_gemm(X, sorted_idx, offsets, 1, kt, T, w, G, K, N, g, 0, y_buf, stream);
+  if (rc) return rc;
+  return combine(y_buf, probs, inverse, T, kt, k, 1.0f, nullptr, offsets + G, N, out, stream);
 }
 
 }  // namespace
@@ -609,7 +672,7 @@ extern "C" int mm_moe_grouped_gemm(const uint16_t* X, const int32_t* sorted_idx,
 
 extern "C" int mm_moe_combine(const uint16_t* Y, const float* probs, const int32_t* inverse,
                               int T, int k, int H, uint16_t* out, void* stream) {
-  return combine(Y, probs, inverse, T, k, k, 0.0f, nullptr, H, out, stream);
+  return combine(Y, probs, inverse, T, k, k, 0.0f, nullptr, nullptr, H, out, stream);
 }
 
 extern "C" int mm_moe_mlp_fp4(const uint16_t* X, const void* expert_ids, int ids_i64,
@@ -645,4 +708,18 @@ extern "C" int mm_moe_mlp_shared_fp4(const uint16_t* X, const void* expert_ids, 
   return moe_mlp(who, X, (const int32_t*)expert_ids, probs, T, k, E, H, I, Bgu, Sgu, Bdn, Sdn,
                  Bsgu, Ssgu, Bsdn, Ssdn, shared_weight, base, g, act_buf, y_buf, sort_buf, out,
                  stream);
+}
+
+extern "C" int mm_moe_gemm_shared_fp4(const uint16_t* X, const void* expert_ids, int ids_i64,
+                                      const float* probs, int T, int k, int E, int K, int N,
+                                      const uint32_t* Bsh, const uint16_t* Ssh,
+                                      const uint32_t* B, const uint16_t* S, int g,
+                                      uint16_t* y_buf, int32_t* sort_buf, uint16_t* out,
+                                      void* stream) {
+  const char* who = "mm_moe_gemm_shared_fp4";
+  if (ids_i64 || k == 0)
+    return moe_gemm_shared(who, X, (const int64_t*)expert_ids, probs, T, k, E, K, N, Bsh, Ssh,
+                           B, S, g, y_buf, sort_buf, out, stream);
+  return moe_gemm_shared(who, X, (const int32_t*)expert_ids, probs, T, k, E, K, N, Bsh, Ssh, B,
+                         S, g, y_buf, sort_buf, out, stream);
 }

@@ -17,7 +17,8 @@ from .ops import GemmFp4, dispatch_gemm_fp4
 from .loader import QuantizedModel, convert_safetensors_to_fp4, load_and_quantize_safetensors
 from .moe_dispatch import (FusedMoEDispatcher, MoEDispatcher, _fused_expert_mlp,
                            dispatch_experts_batched, moe_add_shared_expert_fp4,
-                           moe_fused_dispatch_shared_fp4, moe_shared_expert_fp4, MoEDispatchInfo, compute_expert_load,
+                           moe_fused_dispatch_shared_fp4, moe_shared_expert_fp4,
+                           moe_shared_expert_fused_fp4, MoEDispatchInfo, compute_expert_load,
                            compute_load_balancing_loss, gather_for_experts,
                            group_tokens_by_expert, group_tokens_by_expert_full,
                            fused_router_topk, mmfp4_softmax_topk, moe_expert_gemm_fp4,

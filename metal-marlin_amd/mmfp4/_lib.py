@@ -54,6 +54,8 @@ SIGNATURES: dict[str, tuple] = {
     "mm_moe_mlp_shared_fp4": (_c_int, [_vp, _vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_int,
                                        _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                        ctypes.c_float, _vp, _c_int, _vp, _vp, _vp, _vp, _vp]),
+    "mm_moe_gemm_shared_fp4": (_c_int, [_vp, _vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_int,
+                                        _c_int, _vp, _vp, _vp, _vp, _c_int, _vp, _vp, _vp, _vp]),
     "mm_fp4_flat_quantize": (_c_int, [_vp, _c_size, _c_int, _c_int, _vp, _vp, _vp]),
     "mm_fp4_flat_dequantize": (_c_int, [_vp, _vp, _c_size, _c_size, _c_int, _vp, _vp]),
     "mm_fp4_pack_pair": (_c_int, [_vp, _vp, _c_size, _vp, _vp]),

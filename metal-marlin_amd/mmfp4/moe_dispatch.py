@@ -17,6 +17,8 @@ import torch.nn as nn
 
 from . import _lib
 
+FP4_PER_UINT = 8
+
 
 @dataclass
 class MoEDispatchInfo:
@@ -211,14 +213,18 @@ def moe_fused_router_sorted(hidden_states: torch.Tensor, gate: nn.Linear, top_k:
 
 
 def _grouped(x, sorted_idx, offsets, gather: bool, k: int, T: int, packed, scales,
-             group_size: int, act: int) -> torch.Tensor:
+             group_size: int, act: int, zero_rows: bool = False) -> torch.Tensor:
+    """mm_moe_grouped_gemm -> [T*k, N (N/2 with act)] in sorted order.  Rows
+    of dropped assignments (ids outside [0, E)) are not written by the
+    kernel; zero_rows makes them zero."""
     E, KP, N = packed.shape
     K = KP * 8
     if tuple(scales.shape) != (E, K // group_size, N):
         raise ValueError(f"scales shape {tuple(scales.shape)} != ({E}, {K // group_size}, {N})")
     if x.shape[-1] != K:
         raise ValueError(f"activations K={x.shape[-1]} != packed K={K}")
-    out = torch.empty((T * k, N // 2 if act else N), dtype=torch.float16, device=x.device)
+    alloc = torch.zeros if zero_rows else torch.empty
+    out = alloc((T * k, N // 2 if act else N), dtype=torch.float16, device=x.device)
     _lib.call("mm_moe_grouped_gemm", _lib.ptr(x), _lib.ptr(sorted_idx), _lib.ptr(offsets),
               int(gather), k, T, _lib.ptr(packed.contiguous()), _lib.ptr(scales.contiguous()),
               E, K, N, group_size, act, _lib.ptr(out), _lib.stream_of(x))
@@ -229,18 +235,26 @@ def _half(t: torch.Tensor) -> torch.Tensor:
     return (t if t.dtype == torch.float16 else t.to(torch.float16)).contiguous()
 
 
+def _packed_words(t: torch.Tensor) -> torch.Tensor:
+    if t.dtype not in (torch.int32, torch.uint32):
+        raise TypeError(f"packed weights must be int32/uint32 words, got {t.dtype}")
+    return t.contiguous()
+
+
 def moe_expert_gemm_fp4(activations: torch.Tensor, expert_weights: torch.Tensor,
                         scales: torch.Tensor, expert_ids: torch.Tensor,
                         expert_probs: torch.Tensor, group_size: int = 128) -> torch.Tensor:
     """out[t] = sum_j p[t, j] * (x[t] @ dequant(W[e(t, j)])) (kernels/moe.py:583-727).
     activations [T, K]; expert_weights [E, K/8, N]; scales [E, K/g, N];
-    expert_ids / expert_probs [T, k].  Returns [T, N] in activations' dtype."""
+    expert_ids / expert_probs [T, k].  Returns [T, N] in activations' dtype.
+    Ids outside [0, E) contribute nothing (the reference kernel skips them)."""
     _lib.require_device(activations, expert_weights, scales, expert_ids, expert_probs)
     T, k = expert_ids.shape
     E = expert_weights.shape[0]
     x = _half(activations)
     s_idx, offs, inv = _sort(expert_ids, E)
-    y = _grouped(x, s_idx, offs, True, k, T, expert_weights, _half(scales), group_size, 0)
+    y = _grouped(x, s_idx, offs, True, k, T, expert_weights, _half(scales), group_size, 0,
+                 zero_rows=True)
     info = MoEDispatchInfo(s_idx, s_idx, offs, inv, T, k, E, s_idx)
     out = scatter_expert_outputs(y, expert_probs, info)
     return out.to(activations.dtype)
@@ -446,6 +460,70 @@ def moe_add_shared_expert_fp4(hidden_states: torch.Tensor, moe_output: torch.Ten
                                     shared_down_packed, shared_down_scales),
                           None, None, 1.0, moe_output, group_size)
     return out.reshape(*shape[:-1], out.shape[-1])
+
+
+def moe_shared_expert_fused_fp4(hidden_states: torch.Tensor, shared_expert_packed: torch.Tensor,
+                                shared_expert_scales: torch.Tensor,
+                                routed_expert_packed: torch.Tensor,
+                                routed_expert_scales: torch.Tensor, router_probs: torch.Tensor,
+                                router_indices: torch.Tensor,
+                                group_size: int = 128) -> torch.Tensor:
+    """Shared + routed aggregation of one FP4 projection (kernels/moe.py:
+    182-329, src/moe_shared_expert.metal:604-):
+        out[t] = x[t] @ W_sh + sum_j p[t, j] * (x[t] @ W_{e(t, j)})
+    shared_expert_packed [H/8, I] Marlin layout, scales [H/g, I]; routed
+    [E, H/8, I] / [E, H/g, I]; router_probs / router_indices [T, top_k].
+    Indices outside [0, E) contribute nothing (the reference kernel skips
+    them).  One library call: the shared matrix is one more group of the
+    grouped launch.  fp16 [..., I]."""
+    x, shape = _flatten_hidden(hidden_states)
+    T, H = x.shape
+    if H % FP4_PER_UINT != 0:
+        raise ValueError(f"hidden_dim ({H}) must be divisible by {FP4_PER_UINT}")
+    if H % group_size != 0:
+        raise ValueError(f"hidden_dim ({H}) must be divisible by group_size ({group_size})")
+    if shared_expert_packed.dim() != 2:
+        raise ValueError("shared_expert_packed must be [hidden/8, intermediate]")
+    packed_k = int(shared_expert_packed.shape[0])
+    if packed_k * FP4_PER_UINT != H:
+        raise ValueError("shared_expert_packed hidden dim mismatch")
+    I = int(shared_expert_packed.shape[1])
+    rows = H // group_size
+    if tuple(shared_expert_scales.shape) != (rows, I):
+        raise ValueError("shared_expert_scales shape mismatch")
+    if routed_expert_packed.dim() != 3:
+        raise ValueError("routed_expert_packed must be [num_experts, hidden/8, intermediate]")
+    if routed_expert_packed.shape[1] != packed_k or routed_expert_packed.shape[2] != I:
+        raise ValueError("routed_expert_packed shape mismatch")
+    if routed_expert_scales.dim() != 3:
+        raise ValueError("routed_expert_scales must be [num_experts, hidden/group, intermediate]")
+    if routed_expert_scales.shape[1] != rows or routed_expert_scales.shape[2] != I:
+        raise ValueError("routed_expert_scales shape mismatch")
+    if router_probs.dim() != 2 or router_probs.shape[0] != T:
+        raise ValueError("router_probs must be [tokens, top_k]")
+    if router_indices.dim() != 2 or router_indices.shape[0] != T:
+        raise ValueError("router_indices must be [tokens, top_k]")
+    k = int(router_probs.shape[1])
+    if router_indices.shape[1] != k:
+        raise ValueError("router_probs and router_indices must have same top_k")
+    if I % 8 != 0:
+        raise ValueError(f"intermediate_dim ({I}) must be divisible by 8")
+    dev = _lib.require_device(x, shared_expert_packed, shared_expert_scales, routed_expert_packed,
+                              routed_expert_scales, router_probs, router_indices)
+    E = int(routed_expert_packed.shape[0])
+    i64 = int(router_indices.dtype == torch.int64)
+    ids = router_indices.contiguous() if i64 else router_indices.to(torch.int32).contiguous()
+    p = router_probs.to(torch.float32).contiguous()
+    sp, rp = _packed_words(shared_expert_packed), _packed_words(routed_expert_packed)
+    ss, rs = _half(shared_expert_scales), _half(routed_expert_scales)
+    kt = k + 1
+    y = torch.empty((T * kt, I), dtype=torch.float16, device=dev)
+    sort_buf = torch.empty(E + 2 + 2 * T * kt, dtype=torch.int32, device=dev)
+    out = torch.empty((T, I), dtype=torch.float16, device=dev)
+    _lib.call("mm_moe_gemm_shared_fp4", _lib.ptr(x), _lib.ptr(ids), i64, _lib.ptr(p), T, k, E,
+              H, I, _lib.ptr(sp), _lib.ptr(ss), _lib.ptr(rp), _lib.ptr(rs), group_size,
+              _lib.ptr(y), _lib.ptr(sort_buf), _lib.ptr(out), _lib.stream_of(x))
+    return out.reshape(*shape[:-1], I)
 
 
 def moe_fused_dispatch_shared_fp4(hidden_states: torch.Tensor,

@@ -154,3 +154,79 @@ def test_dispatch_experts_batched(rng, T, k):
     a, b = int(off[e0]), int(off[e0 + 1])
     ref[a:b] = omoe.expert_mlp_ref(xs_ref[a:b], GU[e0], GS[e0], new_dp, new_ds, g)
     assert max_abs_rel(to_np(y2), ref) <= TOL
+
+
+def _proj(rng, K, N, g):
+    w = rng.normal(0, 0.02, (N, K)).astype(np.float16)
+    return ofp4.quantize_fp4(w, g)                 # [K/8, N], [K/g, N]
+
+
+@pytest.mark.parametrize("T,E,k,i64", [(32, 16, 4, False), (512, 8, 2, True), (1, 4, 3, False)])
+def test_shared_expert_fused_fp4(rng, T, E, k, i64):
+    """moe_shared_expert_fused_fp4 (kernels/moe.py:182-329): one projection,
+    out = x @ W_sh + sum_j p_j x @ W_e(j), against the fp32 brute force; one
+    slot per token is given an out-of-range id, which contributes nothing
+    (T=512 gives the routed groups prefill-sized row counts)."""
+    import mmfp4
+    H, I, g = 512, 256, 128
+    sp, ss = _proj(rng, H, I, g)
+    parts = [_proj(rng, H, I, g) for _ in range(E)]
+    RP, RS = np.stack([q[0] for q in parts]), np.stack([q[1] for q in parts])
+    x = rng.normal(0, 1, (T, H)).astype(np.float16)
+    ids, probs = omoe.router_topk(rng.normal(0, 1, (T, E)), k)
+    ids = ids.astype(np.int64)
+    ids[:, -1] = np.where(np.arange(T) % 2 == 0, -1, E)       # dropped slots
+    ref = ofp4.gemm_fp4_ref(x, sp, ss, g).astype(np.float32)
+    for t in range(T):
+        for j in range(k):
+            e = int(ids[t, j])
+            if 0 <= e < E:
+                ref[t] += probs[t, j] * ofp4.gemm_fp4_ref(x[t:t + 1], RP[e], RS[e], g)[0]
+    dids = to_dev(ids if i64 else ids.astype(np.int32))
+    announce(f"moe_shared_expert_fused_fp4 T={T} E={E} k={k} i64={i64}")
+    out = mmfp4.moe_shared_expert_fused_fp4(to_dev(x.reshape(1, T, H)), to_dev(sp), to_dev(ss),
+                                            to_dev(RP), to_dev(RS), to_dev(probs), dids, g)
+    assert out.shape == (1, T, I) and out.dtype == torch.float16
+    assert max_abs_rel(to_np(out[0]), ref) <= TOL
+
+
+@pytest.mark.parametrize("T,E,k", [(32, 16, 4), (600, 8, 2)])
+def test_dropped_expert_ids(rng, T, E, k):
+    """Ids outside [0, E): the sort places them after every expert's rows in
+    index order (the stable argsort of the ids with those mapped to E), and
+    offsets[E] counts the valid ones; moe_mlp_fp4 and moe_expert_gemm_fp4
+    give them no contribution."""
+    import mmfp4
+    H, I, g = 256, 128, 128
+    ids, probs = omoe.router_topk(rng.normal(0, 1, (T, E)), k)
+    ids = ids.astype(np.int64)
+    bad = rng.random((T, k)) < 0.2
+    ids[bad] = rng.choice([-1, -7, E, E + 5, 1 << 40], size=int(bad.sum()))
+    announce(f"dropped ids sort T={T} E={E} k={k}")
+    s, o, inv = mmfp4.group_tokens_by_expert(to_dev(ids), E)
+    keys = np.where((ids >= 0) & (ids < E), ids, E).reshape(-1)
+    want = np.argsort(keys, kind="stable")
+    assert np.array_equal(to_np(s), want)
+    assert np.array_equal(to_np(inv)[want], np.arange(T * k))
+    cnt = np.bincount(keys, minlength=E + 1)
+    assert np.array_equal(to_np(o), np.concatenate([[0], np.cumsum(cnt[:E])]))
+    # the MLP and the single-projection entry: dropped slots contribute zero
+    GU, GS, DP, DS = _experts(rng, E, H, I, g)
+    x = rng.normal(0, 1, (T, H)).astype(np.float16)
+    safe = np.where(bad, 0, ids).astype(np.int32)
+    p0 = np.where(bad, 0.0, probs).astype(np.float32)
+    ref = omoe.moe_forward_ref(x, GU, GS, DP, DS, safe, p0, g)
+    out = mmfp4.moe_mlp_fp4(to_dev(x), to_dev(GU), to_dev(GS), to_dev(DP), to_dev(DS),
+                            to_dev(ids), to_dev(probs), g)
+    assert max_abs_rel(to_np(out), ref) <= TOL
+    WP, WS = GU[:, :, :I], np.ascontiguousarray(GS[:, :, :I])
+    WP = np.ascontiguousarray(WP)
+    ref1 = np.zeros((T, I), np.float32)
+    for t in range(T):
+        for j in range(k):
+            if not bad[t, j]:
+                ref1[t] += probs[t, j] * ofp4.gemm_fp4_ref(x[t:t + 1], WP[ids[t, j]],
+                                                           WS[ids[t, j]], g)[0]
+    out1 = mmfp4.moe_expert_gemm_fp4(to_dev(x), to_dev(WP), to_dev(WS), to_dev(ids),
+                                     to_dev(probs), g)
+    assert max_abs_rel(to_np(out1), ref1) <= TOL
