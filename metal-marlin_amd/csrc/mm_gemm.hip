@@ -74,8 +74,12 @@ k_skinny(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
   static_assert(ACT == SK_PLAIN || ACT == SK_MULTI || NT == 2,
                 "pair modes use one tile of each matrix");
   constexpr bool ONE = ACT == SK_PLAIN || ACT == SK_MULTI;   // one matrix per block
+  // Row-packed weights are staged through 8 KiB of LDS per wave and tile in
+  // the main loop; the block reduction reuses the same memory afterwards.
+  constexpr bool STAGE = ROWP == 1 || ROWP == 2;
   constexpr int RED = (NW > 1 ? NW - 1 : 1) * MT * NT * 16 * 64;
-  __shared__ float red[RED];
+  constexpr int LDSF = STAGE && NW * NT * 2048 > RED ? NW * NT * 2048 : RED;   // floats
+  __shared__ __attribute__((aligned(16))) float red[LDSF];
   __shared__ uint32_t s_last;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int c = lane & 15, q = lane >> 4;
@@ -115,8 +119,10 @@ k_skinny(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
                 : (t == 0 ? SkTile{B, S, Z, n0} : SkTile{B2, S2, Z2, n0});
   if constexpr (ROWP == 1 || ROWP == 2) {
     static_assert(!INT4 && ACT != SK_MULTI, "row-packed: FP4 product or gate/up pair");
-    rowp_wave<MT, NT, SPW, ROWP == 2>(A, lda, M, tl, N, K, g, blk_st0 + wave * SPW, nrounds,
-                                      NW * SPW, acc);
+    rowp_wave<MT, NT, SPW, ROWP == 2, false, STAGE>(A, lda, M, tl, N, K, g, blk_st0 + wave * SPW,
+                                                    nrounds, NW * SPW, acc,
+                                                    (char*)red + wave * NT * 8192);
+    if constexpr (STAGE) __syncthreads();   // every wave is done with its staging area
   } else {
     skinny_wave<INT4, MT, NT, SPW, FL, false, ROWP == 3>(A, lda, nullptr, 1, M, tl, N, K, g,
                                                          blk_st0 + wave * SPW, nrounds, NW * SPW,
@@ -255,7 +261,11 @@ __global__ void __launch_bounds__(NW * 64)
 k_skinny_dual(const f16* __restrict__ A, const uint32_t* __restrict__ B,
               const f16* __restrict__ S, const f16* __restrict__ Z, f16* __restrict__ C, int M,
               int N, int K, int g, int nrounds) {
-  __shared__ float red[(NW - 1) * 16 * 64];
+  // ROWP: each wave stages its weights through 8 KiB of LDS in the main
+  // loop; the block reduction reuses the same memory afterwards.
+  constexpr int RED = (NW - 1) * 16 * 64;
+  constexpr int LDSF = ROWP && NW * 2048 > RED ? NW * 2048 : RED;   // floats
+  __shared__ __attribute__((aligned(16))) float red[LDSF];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int c = lane & 15, q = lane >> 4;
   const int n0 = blockIdx.x * 32;
@@ -263,9 +273,11 @@ k_skinny_dual(const f16* __restrict__ A, const uint32_t* __restrict__ B,
 #pragma unroll
   for (int j = 0; j < 4; ++j) acc[0][0][j] = f32x4{0, 0, 0, 0};
   const SkTile tl[1] = {SkTile{B, S, Z, n0}};
-  if constexpr (ROWP)
-    rowp_wave<1, 1, SPW, !SROW, true>(A, K, M, tl, N, K, g, wave * SPW, nrounds, NW * SPW, acc);
-  else
+  if constexpr (ROWP) {
+    rowp_wave<1, 1, SPW, !SROW, true, true>(A, K, M, tl, N, K, g, wave * SPW, nrounds, NW * SPW,
+                                            acc, (char*)red + wave * 8192);
+    __syncthreads();   // every wave is done with its staging area
+  } else
     skinny_wave<INT4, 1, 1, SPW, FL, true, SROW>(A, K, nullptr, 1, M, tl, N, K, g, wave * SPW,
                                                  nrounds, NW * SPW, acc);
   // Rows 8..15 (lanes q >= 2) hold the second slab's sums: reduce all 16.

@@ -280,10 +280,23 @@ MM_DEV void skinny_wave(const f16* __restrict__ A, int lda, const int* __restric
 // DUAL (M <= 8, K % 512 == 0): a step is 64 k and a round 64 word rows; lanes
 // c < 8 take the round's first 32 rows and lanes c >= 8 the next 32, for the
 // 32 columns of lane group c & 7 (the two-slab scheme of skinny_wave).
-template <int MT, int NT, int SPW, bool SG, bool DUAL = false>
+MM_DEV void stage_load16(const void* src, void* lds_base_uniform) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds_base_uniform,
+                                   16, 0, 0);
+}
+
+// STAGE: the round's words are first copied global -> LDS with whole
+// 128-byte lines per column (8 lanes per line, 8 columns per load
+// instruction) into the wave's 8 KiB region per tile (`stage` + 8 KiB * t),
+// then read back in the lanes' layout.  16-byte piece p of LDS column x (the wave's x-th column,
+// p = word row / 4 within the round) lives at slot
+//   PPC * x' + (p ^ ((x >> 2) & 7)),  x' = DUAL ? x : x ^ ((x >> 5) & 1),
+// PPC = pieces per column (8, or 16 for DUAL), so the 16 lanes of a read
+// pass (16 columns, one piece each) hit 16 different bank groups.
+template <int MT, int NT, int SPW, bool SG, bool DUAL = false, bool STAGE = false>
 MM_DEV void rowp_wave(const f16* __restrict__ A, int lda, int M, const SkTile (&tl)[NT], int N,
                       int K, int g, int st0, int nrounds, int ststride,
-                      f32x4 (&acc)[MT][NT][4]) {
+                      f32x4 (&acc)[MT][NT][4], char* stage = nullptr) {
   // SG: scales groups-first [K/g, N] (else [N, K/g]).  NT tiles (gate and up
   // matrices of a pair) share the activations.
   static_assert(SPW == 8, "a lane's run of rows is one 64-k piece of a scale group");
@@ -319,22 +332,57 @@ MM_DEV void rowp_wave(const f16* __restrict__ A, int lda, int M, const SkTile (&
       }
     }
     u32x4 w[NT][4][SPW / 4];                                    // [tile][column][4 rows]
+    constexpr int PPC = DUAL ? 16 : 8;                          // 16-byte pieces per column
+    if constexpr (STAGE) {
+      const uint32_t kb = DUAL ? (uint32_t)(8 * stb) : (uint32_t)(4 * stb);   // round's row 0
 #pragma unroll
-    for (int t = 0; t < NT; ++t)
+      for (int t = 0; t < NT; ++t)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+        for (int i = 0; i < 8; ++i) {
+          const int sl = 64 * i + lane;
+          const int xp = sl / PPC, pp = sl % PPC;
+          const int x = DUAL ? xp : (xp ^ ((xp >> 5) & 1));
+          const int p = pp ^ ((x >> 2) & 7);
+          const uint32_t cg = (uint32_t)min(tl[t].col0 + x, N - 1);
+          stage_load16(at_bytes<u32x4>(tl[t].B, (cg * (uint32_t)KP + kb + 4u * p) * 4u),
+                       stage + 8192 * t + 1024 * i);
+        }
+    } else {
 #pragma unroll
-        for (int u = 0; u < SPW / 4; ++u)
-          // Plain loads: the two 16-byte pieces of a lane share 128-byte lines
-          // with the neighbouring lanes' pieces, read by the next instruction;
-          // a non-temporal hint made the layer GEMMs ~15% slower (4096x28672
-          // at M=1 21.5 -> 18.4 us without it).
-          w[t][j][u] = *at_bytes<u32x4>(tl[t].B, ((col[t] + j) * (uint32_t)KP + kp0 + 4u * u) * 4u);
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int u = 0; u < SPW / 4; ++u)
+            // Plain loads: the two 16-byte pieces of a lane share 128-byte lines
+            // with the neighbouring lanes' pieces, read by the next instruction;
+            // a non-temporal hint made the layer GEMMs ~15% slower (4096x28672
+            // at M=1 21.5 -> 18.4 us without it).
+            w[t][j][u] = *at_bytes<u32x4>(tl[t].B, ((col[t] + j) * (uint32_t)KP + kp0 + 4u * u) * 4u);
+    }
     f16x8 a[SPW][MT];
 #pragma unroll
     for (int i = 0; i < SPW; ++i)
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) a[i][mt] = *at_bytes<f16x8>(A, aoff[mt] + (kp0 + i) * 16u);
+    if constexpr (STAGE) {
+      // This wave's copies have landed (vmcnt counts them in issue order with
+      // the activation and scale loads).
+      __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));   // vmcnt(0)
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int x = (int)(col[t] - (uint32_t)tl[t].col0) + j;
+          const int xp = DUAL ? x : (x ^ ((x >> 5) & 1));
+#pragma unroll
+          for (int u = 0; u < SPW / 4; ++u) {
+            const int p = DUAL ? 8 * hs + 2 * q + u : 2 * q + u;
+            w[t][j][u] =
+                *(const u32x4*)(stage + 8192 * t + (PPC * xp + (p ^ ((x >> 2) & 7))) * 16);
+          }
+        }
+    }
 #pragma unroll
     for (int i = 0; i < SPW; ++i)
 #pragma unroll
