@@ -107,3 +107,58 @@ def test_fuzz_rowpacked(M, K, N, g):
     assert torch.equal(out_t.view(torch.int16), out.view(torch.int16))
     pair = mmfp4.mmfp4_fused_gate_up(a, rg, gs, ru, us, g)
     assert max_abs_rel(to_np(pair), to_np(torch.nn.functional.silu(hg) * hu)) <= TOL
+
+
+def _moe_shapes(seed, n):
+    r = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        g = int(r.choice([32, 64, 128]))
+        H = g * int(r.integers(1, max(2, 1024 // g)))
+        I = g * int(r.integers(1, max(2, 512 // g)))
+        if H % 8 or I % 8:
+            continue
+        E = int(r.choice([1, 3, 8, 17, 64]))
+        k = int(r.integers(1, min(E, 8) + 1))
+        T = int(r.choice([1, 5, 32, 97, 300, 700]))
+        out.append((T, E, k, H, I, g))
+    return out
+
+
+@pytest.mark.parametrize("T,E,k,H,I,g", _moe_shapes(2024, 12))
+def test_fuzz_moe_mlp(T, E, k, H, I, g):
+    """Seeded random MoE shapes (decode- and prefill-sized groups, K not a
+    multiple of 64, int32 and int64 ids, a few out-of-range ids) through
+    moe_mlp_fp4, against an fp32 torch reference built from the bit-exact
+    dequant: sum_j p_j * SwiGLU-MLP_{e_j}(x), dropped slots contributing 0."""
+    import mmfp4
+    gen = torch.Generator(device="cuda").manual_seed(T * 7 + E * 3 + H + I + k)
+    gp, gs, dp, ds = [], [], [], []
+    for _ in range(E):
+        w = (torch.randn((2 * I, H), generator=gen, device="cuda") * 0.02).half()
+        p, s = mmfp4.quantize_fp4(w, group_size=g)
+        gp.append(p); gs.append(s)
+        w = (torch.randn((H, I), generator=gen, device="cuda") * 0.02).half()
+        p, s = mmfp4.quantize_fp4(w, group_size=g)
+        dp.append(p); ds.append(s)
+    GP, GS, DP, DS = (torch.stack(v) for v in (gp, gs, dp, ds))
+    x = torch.randn((T, H), generator=gen, device="cuda").half()
+    logits = torch.randn((T, E), generator=gen, device="cuda")
+    probs, ids = torch.topk(torch.softmax(logits, -1), k, -1)
+    probs = probs / probs.sum(-1, keepdim=True)
+    drop = torch.rand((T, k), generator=gen, device="cuda") < 0.05
+    ids = torch.where(drop, torch.full_like(ids, E + 3), ids)
+    if T % 2:
+        ids = ids.to(torch.int32)
+    ref = torch.zeros((T, H), dtype=torch.float32, device="cuda")
+    xf = x.float()
+    for e in range(E):
+        wgu = mmfp4.dequant_fp4(GP[e], GS[e], H, 2 * I, g).float()
+        wdn = mmfp4.dequant_fp4(DP[e], DS[e], I, H, g).float()
+        h = xf @ wgu
+        y = (torch.nn.functional.silu(h[:, :I]) * h[:, I:]) @ wdn
+        w_e = (probs * (ids == e)).sum(-1, keepdim=True)
+        ref += w_e * y
+    announce(f"fuzz moe T={T} E={E} k={k} H={H} I={I} g={g}")
+    out = mmfp4.moe_mlp_fp4(x, GP, GS, DP, DS, ids, probs, g)
+    assert max_abs_rel(to_np(out), to_np(ref)) <= TOL
