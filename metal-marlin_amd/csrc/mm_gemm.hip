@@ -77,8 +77,15 @@ k_skinny(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
   // Row-packed weights are staged through 8 KiB of LDS per wave and tile in
   // the main loop; the block reduction reuses the same memory afterwards.
   constexpr bool STAGE = ROWP == 1 || ROWP == 2;
+  // 9..32 rows, one column tile: each wave's activation slab (16*MT rows x
+  // 32*SPW k, 8 KiB) goes through LDS too, when every round lies inside K
+  // (measured on MI355X, per Llama layer: M=16 46.6 -> 44.6 us, M=32
+  // 69.7 -> 66.4 us; two-tile blocks, e.g. 4096 x 28672 at M=32, were slower
+  // with it, 21.0 -> 22.0 us).
+  constexpr bool ASTG = !STAGE && NT == 1 && 16 * MT * 4 * SPW == 512;
   constexpr int RED = (NW > 1 ? NW - 1 : 1) * MT * NT * 16 * 64;
-  constexpr int LDSF = STAGE && NW * NT * 2048 > RED ? NW * NT * 2048 : RED;   // floats
+  constexpr int STG = STAGE ? NW * NT * 2048 : (ASTG ? NW * 2048 : 0);
+  constexpr int LDSF = STG > RED ? STG : RED;   // floats
   __shared__ __attribute__((aligned(16))) float red[LDSF];
   __shared__ uint32_t s_last;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -123,6 +130,11 @@ k_skinny(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
                                                     nrounds, NW * SPW, acc,
                                                     (char*)red + wave * NT * 8192);
     if constexpr (STAGE) __syncthreads();   // every wave is done with its staging area
+  } else if (ASTG && M > 8 && K % (32 * SPW) == 0) {
+    skinny_wave<INT4, MT, NT, SPW, FL, false, ROWP == 3, ASTG>(
+        A, lda, nullptr, 1, M, tl, N, K, g, blk_st0 + wave * SPW, nrounds, NW * SPW, acc,
+        (char*)red + wave * 8192);
+    __syncthreads();   // every wave is done with its staging area
   } else {
     skinny_wave<INT4, MT, NT, SPW, FL, false, ROWP == 3>(A, lda, nullptr, 1, M, tl, N, K, g,
                                                          blk_st0 + wave * SPW, nrounds, NW * SPW,

@@ -119,11 +119,30 @@ struct SkTile {
 // addresses are clamped into the matrix so no load is predicated.
 // SROW: scales (and zeros) stored [N, K/g] (the reference MMFP4 kernel's
 // layout) instead of [K/g, N]: the four columns' values are four 2-byte loads.
-template <bool INT4, int MT, int NT, int SPW, int FL, bool DUAL = false, bool SROW = false>
+// Asynchronous 16-byte copy global -> LDS (lane l writes lds_base + 16 l).
+MM_DEV void stage_load16(const void* src, void* lds_base_uniform) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds_base_uniform,
+                                   16, 0, 0);
+}
+
+// ASTG (16*MT rows x SPW steps = 8 KiB, no row map, every round inside K):
+// each round's activation slab -- 16*MT rows x 32*SPW k (DUAL: 8 rows x
+// 512 k) -- is loaded with whole lines (whole row segments per load
+// instruction), written to the wave's LDS region `astage`, and the MFMA
+// operands are read back from there.  Loaded directly, each operand load
+// touched 16 rows' half-lines.  16-byte piece p of row r (p = word row within
+// the round) lives at slot PPR * r + (p ^ sw(r)), PPR = 4*SPW (DUAL: 64)
+// pieces per row, sw(r) = r % 16 (DUAL: bits 0, 1, 3 from r's bits 0, 1, 2),
+// so the 16 lanes of a read pass hit 16 bank groups.
+template <bool INT4, int MT, int NT, int SPW, int FL, bool DUAL = false, bool SROW = false,
+          bool ASTG = false>
 MM_DEV void skinny_wave(const f16* __restrict__ A, int lda, const int* __restrict__ rowmap,
                         int rowdiv, int M, const SkTile (&tl)[NT], int N, int K, int g,
-                        int st0, int nrounds, int ststride, f32x4 (&acc)[MT][NT][4]) {
+                        int st0, int nrounds, int ststride, f32x4 (&acc)[MT][NT][4],
+                        char* astage = nullptr) {
   static_assert(FL == 0 || (SPW % FL == 0), "flush interval must divide the round");
+  static_assert(!ASTG || (DUAL ? 8 * 64 : 16 * MT * 4 * SPW) == 512,
+                "activation staging: an 8 KiB slab per wave");
   const int lane = threadIdx.x & 63;
   const int c = lane & 15, q = lane >> 4;
   // DUAL: a step is 64 k; lanes c < 8 take its first 32-k slab and lanes
@@ -167,6 +186,20 @@ MM_DEV void skinny_wave(const f16* __restrict__ A, int lda, const int* __restric
         }
       }
     }
+    constexpr int PPR = DUAL ? 64 : 4 * SPW;   // ASTG: 16-byte pieces per row
+    f16x8 ast[ASTG ? 8 : 1];                // ASTG: this lane's 8 slab pieces
+    if constexpr (ASTG) {
+      const uint32_t kb = (uint32_t)(4 * SLAB * stb);   // round's first word row
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int sl = 64 * i + lane;
+        const int r = sl / PPR, pp = sl % PPR;
+        const int sw = DUAL ? ((r & 3) | ((r & 4) << 1)) : (r & 15) % PPR;
+        const int p = pp ^ sw;
+        ast[i] = *at_bytes<f16x8>(A, (uint32_t)min(r, M - 1) * (uint32_t)lda * 2u +
+                                         (kb + (uint32_t)p) * 16u);
+      }
+    }
 #pragma unroll
     for (int i = 0; i < SPW; ++i) {
       const int kp = min(4 * (SLAB * min(stb + i, nsteps - 1) + hs) + q, KP - 1);
@@ -174,13 +207,32 @@ MM_DEV void skinny_wave(const f16* __restrict__ A, int lda, const int* __restric
       for (int t = 0; t < NT; ++t)
         w[i][t] = __builtin_nontemporal_load(
             at_bytes<u32x4>(tl[t].B, ((uint32_t)kp * (uint32_t)N + coff[t]) * 4u));
+      if constexpr (!ASTG) {
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-        a[i][mt] = *at_bytes<f16x8>(A, aoff[mt] + (uint32_t)kp * 16u);
+        for (int mt = 0; mt < MT; ++mt)
+          a[i][mt] = *at_bytes<f16x8>(A, aoff[mt] + (uint32_t)kp * 16u);
+      }
+    }
+    if constexpr (ASTG) {
+      // Through the wave's LDS region into the lanes' operand layout (the
+      // region is the wave's own: no barrier).
+#pragma unroll
+      for (int i = 0; i < 8; ++i) *(f16x8*)(astage + 1024 * i + 16 * lane) = ast[i];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int r = 16 * mt + cl;          // rows >= M hold a duplicate of row M-1
+        const int sw = DUAL ? ((r & 3) | ((r & 4) << 1)) : (r & 15) % PPR;
+#pragma unroll
+        for (int i = 0; i < SPW; ++i) {
+          const int p = 4 * (SLAB * i + hs) + q;
+          a[i][mt] = *(const f16x8*)(astage + (PPR * r + (p ^ sw)) * 16);
+        }
+      }
     }
     // Steps past K (a partial last step, or a round overhanging the end)
-    // contribute zero through a zeroed activation operand.
-    if (stb + SPW > nsteps || (K & (32 * SLAB - 1)) != 0) {
+    // contribute zero through a zeroed activation operand.  (ASTG rounds lie
+    // inside K.)
+    if (!ASTG && (stb + SPW > nsteps || (K & (32 * SLAB - 1)) != 0)) {
 #pragma unroll
       for (int i = 0; i < SPW; ++i) {
         const bool valid = stb + i < nsteps && 4 * (SLAB * (stb + i) + hs) + q < KP;
@@ -280,10 +332,6 @@ MM_DEV void skinny_wave(const f16* __restrict__ A, int lda, const int* __restric
 // DUAL (M <= 8, K % 512 == 0): a step is 64 k and a round 64 word rows; lanes
 // c < 8 take the round's first 32 rows and lanes c >= 8 the next 32, for the
 // 32 columns of lane group c & 7 (the two-slab scheme of skinny_wave).
-MM_DEV void stage_load16(const void* src, void* lds_base_uniform) {
-  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds_base_uniform,
-                                   16, 0, 0);
-}
 
 // STAGE: the round's words are first copied global -> LDS with whole
 // 128-byte lines per column (8 lanes per line, 8 columns per load
@@ -366,8 +414,8 @@ MM_DEV void rowp_wave(const f16* __restrict__ A, int lda, int M, const SkTile (&
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) a[i][mt] = *at_bytes<f16x8>(A, aoff[mt] + (kp0 + i) * 16u);
     if constexpr (STAGE) {
-      // This wave's copies have landed (vmcnt counts them in issue order with
-      // the activation and scale loads).
+      // Wait for every vector load of the round: the compiler may issue the
+      // activation loads before the copies, so no partial count is safe.
       __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));   // vmcnt(0)
 #pragma unroll
       for (int t = 0; t < NT; ++t)
