@@ -63,7 +63,9 @@ struct SkMulti {
 // the same columns of (B2, S2, Z2).  Split-K partials are [ksplit][M][PW]
 // fp32 with PW = N, 2N for the pair modes (gate at n, up at N + n), or ntot.
 // ROWP: 0 Marlin-layout weights; row-packed [N, K/8] weights with scales
-// [N, K/g] (1) or [K/g, N] (2); 3 Marlin-layout weights with scales [N, K/g].
+// [N, K/g] (1, 4) or [K/g, N] (2, 5), staged through LDS per tile as loaded
+// (1, 2: rowp_wave) or transposed to the Marlin layout (4, 5: skinny_wave
+// RT); 3 Marlin-layout weights with scales [N, K/g].
 template <bool INT4, int MT, int NT, int SPW, int NW, int FL, int ACT, int ROWP = 0>
 __global__ void __launch_bounds__(NW * 64)
 k_skinny(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
@@ -76,7 +78,7 @@ k_skinny(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
   constexpr bool ONE = ACT == SK_PLAIN || ACT == SK_MULTI;   // one matrix per block
   // Row-packed weights are staged through 8 KiB of LDS per wave and tile in
   // the main loop; the block reduction reuses the same memory afterwards.
-  constexpr bool STAGE = ROWP == 1 || ROWP == 2;
+  constexpr bool STAGE = ROWP == 1 || ROWP == 2 || ROWP == 4 || ROWP == 5;
   // 9..32 rows, one column tile: each wave's activation slab (16*MT rows x
   // 32*SPW k, 8 KiB) goes through LDS too, when every round lies inside K
   // (measured on MI355X, per Llama layer: M=16 46.6 -> 44.6 us, M=32
@@ -124,11 +126,16 @@ k_skinny(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
   for (int t = 0; t < NT; ++t)
     tl[t] = ONE ? SkTile{B, S, Z, n0 + t * SK_COLS}
                 : (t == 0 ? SkTile{B, S, Z, n0} : SkTile{B2, S2, Z2, n0});
-  if constexpr (ROWP == 1 || ROWP == 2) {
+  if constexpr (STAGE) {
     static_assert(!INT4 && ACT != SK_MULTI, "row-packed: FP4 product or gate/up pair");
-    rowp_wave<MT, NT, SPW, ROWP == 2, false, STAGE>(A, lda, M, tl, N, K, g, blk_st0 + wave * SPW,
-                                                    nrounds, NW * SPW, acc,
-                                                    (char*)red + wave * NT * 8192);
+    if constexpr (ROWP <= 2)
+      rowp_wave<MT, NT, SPW, ROWP == 2, false, true>(A, lda, M, tl, N, K, g,
+                                                     blk_st0 + wave * SPW, nrounds, NW * SPW,
+                                                     acc, (char*)red + wave * NT * 8192);
+    else
+      skinny_wave<false, MT, NT, SPW, FL, false, ROWP == 4, false, true>(
+          A, lda, nullptr, 1, M, tl, N, K, g, blk_st0 + wave * SPW, nrounds, NW * SPW, acc,
+          nullptr, (char*)red + wave * NT * 8192);
     if constexpr (STAGE) __syncthreads();   // every wave is done with its staging area
   } else if (ASTG && M > 8 && K % (32 * SPW) == 0) {
     skinny_wave<INT4, MT, NT, SPW, FL, false, ROWP == 3, ASTG>(
@@ -286,8 +293,9 @@ k_skinny_dual(const f16* __restrict__ A, const uint32_t* __restrict__ B,
   for (int j = 0; j < 4; ++j) acc[0][0][j] = f32x4{0, 0, 0, 0};
   const SkTile tl[1] = {SkTile{B, S, Z, n0}};
   if constexpr (ROWP) {
-    rowp_wave<1, 1, SPW, !SROW, true, true>(A, K, M, tl, N, K, g, wave * SPW, nrounds, NW * SPW,
-                                            acc, (char*)red + wave * 8192);
+    skinny_wave<false, 1, 1, SPW, FL, true, SROW, false, true>(
+        A, K, nullptr, 1, M, tl, N, K, g, wave * SPW, nrounds, NW * SPW, acc, nullptr,
+        (char*)red + wave * 8192);
     __syncthreads();   // every wave is done with its staging area
   } else
     skinny_wave<INT4, 1, 1, SPW, FL, true, SROW>(A, K, nullptr, 1, M, tl, N, K, g, wave * SPW,
@@ -741,21 +749,32 @@ int launch_skinny(const f16* A, int lda, const uint32_t* B, const f16* S, const 
   dim3 grid(gx, p.ksplit);
   constexpr int SPW = sk_spw<MT>();
   const int fl = flush_steps(g, SPW);
-#define MM_LAUNCH_SK(FLV)                                                                   \
-  hipLaunchKernelGGL((k_skinny<INT4, MT, NT, SPW, sk_nw<MT>(), FLV, ACT, ROWP>), grid, dim3(sk_nw<MT>() * 64), 0, \
+#define MM_LAUNCH_SK(FLV, RP)                                                               \
+  hipLaunchKernelGGL((k_skinny<INT4, MT, NT, SPW, sk_nw<MT>(), FLV, ACT, RP>), grid, dim3(sk_nw<MT>() * 64), 0, \
                      st, A, lda, B, S, Z, B2, S2, Z2, C, ldc, M, N, K, g, p.nrounds, part,       \
                      counters, mp ? *mp : none)
-  if constexpr (ROWP == 1 || ROWP == 2) {
-    MM_LAUNCH_SK(0);   // pre-scale: rowp_wave applies each lane's own group scale
-  } else {
-    switch (fl) {
-      case 1: MM_LAUNCH_SK(1); break;
-      case 2: MM_LAUNCH_SK(2); break;
-      case 4: MM_LAUNCH_SK(4 <= SPW ? 4 : 0); break;
-      case 8: MM_LAUNCH_SK(8 <= SPW ? 8 : 0); break;
-      default: MM_LAUNCH_SK(0); break;
-    }
+#define MM_LAUNCH_SK_FL(RP)                                                                 \
+  switch (fl) {                                                                             \
+    case 1: MM_LAUNCH_SK(1, RP); break;                                                     \
+    case 2: MM_LAUNCH_SK(2, RP); break;                                                     \
+    case 4: MM_LAUNCH_SK(4 <= SPW ? 4 : 0, RP); break;                                      \
+    case 8: MM_LAUNCH_SK(8 <= SPW ? 8 : 0, RP); break;                                      \
+    default: MM_LAUNCH_SK(0, RP); break;                                                    \
   }
+  // Row-packed weights: the Marlin-layout transpose (RT) path for unsplit
+  // grids; split grids keep the as-loaded staging, whose fewer registers keep
+  // two blocks resident per CU (measured at M=1, 14336 -> 4096: 11.9 against
+  // 13.7 us).
+  if constexpr (ROWP == 1 || ROWP == 2) {
+    if (p.ksplit == 1) {
+      MM_LAUNCH_SK_FL(ROWP + 3)
+    } else {
+      MM_LAUNCH_SK_FL(ROWP)
+    }
+  } else {
+    MM_LAUNCH_SK_FL(ROWP)
+  }
+#undef MM_LAUNCH_SK_FL
 #undef MM_LAUNCH_SK
   MM_CHECK_LAUNCH("gemm(skinny)");
   return 0;
@@ -1180,14 +1199,28 @@ extern "C" int mm_fp4_gemm_rowpacked(const uint16_t* A, const uint32_t* B, const
     // Marlin-layout path also gives it).
     constexpr int NW = 8;
     const int nr = mm_cdiv(K / 64, NW * 8);
-    if (scales_layout == 1)
-      hipLaunchKernelGGL((k_skinny_dual<false, 8, NW, 0, true, true>), dim3(mm_cdiv(N, 32)),
-                         dim3(NW * 64), 0, st, (const f16*)A, B, (const f16*)S, nullptr, (f16*)C,
-                         M, N, K, g, nr);
-    else
-      hipLaunchKernelGGL((k_skinny_dual<false, 8, NW, 0, false, true>), dim3(mm_cdiv(N, 32)),
-                         dim3(NW * 64), 0, st, (const f16*)A, B, (const f16*)S, nullptr, (f16*)C,
-                         M, N, K, g, nr);
+    // 64-k steps per scale group (0: a group size that no whole number of
+    // steps matches -- use_dual excludes it -- decodes with the scale applied).
+    const int fl = flush_steps(g / 2, 8);
+#define MM_LAUNCH_RDU(FLV, SR)                                                                  \
+  hipLaunchKernelGGL((k_skinny_dual<false, 8, NW, FLV, SR, true>), dim3(mm_cdiv(N, 32)),       \
+                     dim3(NW * 64), 0, st, (const f16*)A, B, (const f16*)S, nullptr, (f16*)C, M,  \
+                     N, K, g, nr)
+#define MM_LAUNCH_RDU_FL(SR)                                                                    \
+  switch (fl) {                                                                                \
+    case 1: MM_LAUNCH_RDU(1, SR); break;                                                       \
+    case 2: MM_LAUNCH_RDU(2, SR); break;                                                       \
+    case 4: MM_LAUNCH_RDU(4, SR); break;                                                       \
+    case 8: MM_LAUNCH_RDU(8, SR); break;                                                       \
+    default: MM_LAUNCH_RDU(0, SR); break;                                                      \
+  }
+    if (scales_layout == 1) {
+      MM_LAUNCH_RDU_FL(true)
+    } else {
+      MM_LAUNCH_RDU_FL(false)
+    }
+#undef MM_LAUNCH_RDU_FL
+#undef MM_LAUNCH_RDU
     MM_CHECK_LAUNCH("gemm(rowpacked dual)");
     return 0;
   }

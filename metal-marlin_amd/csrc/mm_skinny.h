@@ -134,12 +134,24 @@ MM_DEV void stage_load16(const void* src, void* lds_base_uniform) {
 // the round) lives at slot PPR * r + (p ^ sw(r)), PPR = 4*SPW (DUAL: 64)
 // pieces per row, sw(r) = r % 16 (DUAL: bits 0, 1, 3 from r's bits 0, 1, 2),
 // so the 16 lanes of a read pass hit 16 bank groups.
+// RT (row-packed weights [N, K/8], FP4, SPW == 8, every round inside K):
+// each round's words -- 32 word rows x 64 columns (DUAL: 64 x 32), 8 KiB
+// per tile -- are loaded with whole lines (a column's 128 or 256 contiguous
+// bytes, 8 or 16 lanes per column) and written to the wave's LDS region
+// `rstage` transposed to the Marlin layout [word row][column], so the rest
+// of the round (the k order, the post-scale decode, the MFMAs) is the
+// Marlin-layout path's.  Word (row r, column x) lives at dword
+// r * W + (x ^ 4 h(r)), W = 64 (DUAL: 32) columns, h(r) = (r >> 2) & 7: the
+// four-column groups a lane reads stay contiguous, the lanes of a read pass
+// hit distinct bank groups, and the transposing stores of one instruction
+// hit 64 (DUAL: 32) distinct banks.
 template <bool INT4, int MT, int NT, int SPW, int FL, bool DUAL = false, bool SROW = false,
-          bool ASTG = false>
+          bool ASTG = false, bool RT = false>
 MM_DEV void skinny_wave(const f16* __restrict__ A, int lda, const int* __restrict__ rowmap,
                         int rowdiv, int M, const SkTile (&tl)[NT], int N, int K, int g,
                         int st0, int nrounds, int ststride, f32x4 (&acc)[MT][NT][4],
-                        char* astage = nullptr) {
+                        char* astage = nullptr, char* rstage = nullptr) {
+  static_assert(!RT || (!INT4 && SPW == 8 && !ASTG), "row-packed staging: FP4, 8 steps");
   static_assert(FL == 0 || (SPW % FL == 0), "flush interval must divide the round");
   static_assert(!ASTG || (DUAL ? 8 * 64 : 16 * MT * 4 * SPW) == 512,
                 "activation staging: an 8 KiB slab per wave");
@@ -200,17 +212,61 @@ MM_DEV void skinny_wave(const f16* __restrict__ A, int lda, const int* __restric
                                          (kb + (uint32_t)p) * 16u);
       }
     }
+    constexpr int RW = DUAL ? 32 : 64;       // RT: columns per tile (dwords per LDS row)
+    constexpr int RPC = DUAL ? 16 : 8;       // RT: 16-byte pieces per column per round
+    u32x4 wp[RT ? NT : 1][RT ? 8 : 1];       // RT: this lane's 8 loaded pieces per tile
+    if constexpr (RT) {
+      const uint32_t kb = (uint32_t)(4 * SLAB * stb);   // round's first word row
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int sl = 64 * i + lane;
+          const int x = sl / RPC, p = sl % RPC;
+          const uint32_t cg = (uint32_t)min(tl[t].col0 + x, N - 1);
+          wp[t][i] = __builtin_nontemporal_load(
+              at_bytes<u32x4>(tl[t].B, (cg * (uint32_t)KP + kb + 4u * (uint32_t)p) * 4u));
+        }
+    }
 #pragma unroll
     for (int i = 0; i < SPW; ++i) {
       const int kp = min(4 * (SLAB * min(stb + i, nsteps - 1) + hs) + q, KP - 1);
+      if constexpr (!RT) {
 #pragma unroll
-      for (int t = 0; t < NT; ++t)
-        w[i][t] = __builtin_nontemporal_load(
-            at_bytes<u32x4>(tl[t].B, ((uint32_t)kp * (uint32_t)N + coff[t]) * 4u));
+        for (int t = 0; t < NT; ++t)
+          w[i][t] = __builtin_nontemporal_load(
+              at_bytes<u32x4>(tl[t].B, ((uint32_t)kp * (uint32_t)N + coff[t]) * 4u));
+      }
       if constexpr (!ASTG) {
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
           a[i][mt] = *at_bytes<f16x8>(A, aoff[mt] + (uint32_t)kp * 16u);
+      }
+    }
+    if constexpr (RT) {
+      // Transpose through the wave's LDS region (its own: no barrier).
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int sl = 64 * i + lane;
+          const int x = sl / RPC, p = sl % RPC;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const int row = 4 * p + k;
+            *(uint32_t*)(rstage + 8192 * t + (row * RW + (x ^ (4 * ((row >> 2) & 7)))) * 4) =
+                wp[t][i][k];
+          }
+        }
+#pragma unroll
+      for (int i = 0; i < SPW; ++i) {
+        const int row = 4 * (SLAB * i + hs) + q;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          const int x0 = (int)(coff[t] - (uint32_t)tl[t].col0);
+          w[i][t] = *(const u32x4*)(rstage + 8192 * t +
+                                   (row * RW + (x0 ^ (4 * ((row >> 2) & 7)))) * 4);
+        }
       }
     }
     if constexpr (ASTG) {
