@@ -108,7 +108,9 @@ k_skinny(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
   const int n0 = tile * (ONE ? NT : 1) * SK_COLS;
   const int ksplit = gridDim.y;
   // First column (lane group c) of tile t in C and in the partial-sum row.
-  auto ccol = [&](int t) { return ONE ? n0 + t * SK_COLS + 4 * c : n0 + 4 * c + (ACT == SK_PAIR ? t * N : 0); };
+  auto ccol = [&](int t) {
+    return ONE ? n0 + t * SK_COLS + 4 * c : n0 + 4 * c + (ACT == SK_PAIR ? t * N : 0);
+  };
   auto pcol = [&](int t) { return ONE ? cbase + n0 + t * SK_COLS + 4 * c : t * N + n0 + 4 * c; };
   // Steps owned by this block: NW*SPW*nrounds consecutive 32-k steps; waves
   // take interleaved SPW-step slabs so each round reads adjacent word rows.
@@ -750,8 +752,8 @@ int launch_skinny(const f16* A, int lda, const uint32_t* B, const f16* S, const 
   constexpr int SPW = sk_spw<MT>();
   const int fl = flush_steps(g, SPW);
 #define MM_LAUNCH_SK(FLV, RP)                                                               \
-  hipLaunchKernelGGL((k_skinny<INT4, MT, NT, SPW, sk_nw<MT>(), FLV, ACT, RP>), grid, dim3(sk_nw<MT>() * 64), 0, \
-                     st, A, lda, B, S, Z, B2, S2, Z2, C, ldc, M, N, K, g, p.nrounds, part,       \
+  hipLaunchKernelGGL((k_skinny<INT4, MT, NT, SPW, sk_nw<MT>(), FLV, ACT, RP>), grid,          \
+                     dim3(sk_nw<MT>() * 64), 0, st, A, lda, B, S, Z, B2, S2, Z2, C, ldc, M, N, K, g, p.nrounds, part,       \
                      counters, mp ? *mp : none)
 #define MM_LAUNCH_SK_FL(RP)                                                                 \
   switch (fl) {                                                                             \
@@ -1291,9 +1293,18 @@ extern "C" int mm_fp4_gate_up_rowpacked(const uint16_t* A, const uint32_t* Bg, c
     }
     const f16 *a = (const f16*)A, *sg = (const f16*)Sg, *su = (const f16*)Su;
     hipStream_t st = (hipStream_t)stream;
-#define MM_LAUNCH_ROWS_PAIR(ACTV)                                                                  switch (p.cfg) {                                                                               case 0:                                                                                        return launch_prefill2<false, ACTV, PF2_BIG, true>(a, K, Bg, sg, nullptr, Bu, su, nullptr,                                                          (f16*)C, ldc, M, N, K, g, p.ksplit,                                                            part, st);                                case 1:                                                                                        return launch_prefill2<false, ACTV, PF2_MID, true>(a, K, Bg, sg, nullptr, Bu, su, nullptr,                                                          (f16*)C, ldc, M, N, K, g, p.ksplit,                                                            part, st);                                default:                                                                                       return launch_prefill2<false, ACTV, PF2_SMALL, true>(a, K, Bg, sg, nullptr, Bu, su,                                                                 nullptr, (f16*)C, ldc, M, N, K, g,                                                             p.ksplit, part, st);                  }
-    if (act) MM_LAUNCH_ROWS_PAIR(SK_SWIGLU)
-    MM_LAUNCH_ROWS_PAIR(SK_PAIR)
+#define MM_LAUNCH_ROWS_PAIR(ACTV, CFG)                                                       \
+  return launch_prefill2<false, ACTV, CFG, true>(a, K, Bg, sg, nullptr, Bu, su, nullptr,       \
+                                                 (f16*)C, ldc, M, N, K, g, p.ksplit, part, st)
+#define MM_LAUNCH_ROWS_PAIR_CFG(ACTV)                                                        \
+  switch (p.cfg) {                                                                           \
+    case 0: MM_LAUNCH_ROWS_PAIR(ACTV, PF2_BIG);                                              \
+    case 1: MM_LAUNCH_ROWS_PAIR(ACTV, PF2_MID);                                              \
+    default: MM_LAUNCH_ROWS_PAIR(ACTV, PF2_SMALL);                                           \
+  }
+    if (act) MM_LAUNCH_ROWS_PAIR_CFG(SK_SWIGLU)
+    MM_LAUNCH_ROWS_PAIR_CFG(SK_PAIR)
+#undef MM_LAUNCH_ROWS_PAIR_CFG
 #undef MM_LAUNCH_ROWS_PAIR
   }
   if (act)
