@@ -75,7 +75,7 @@ def test_layer_gemms_graph_replay(M):
         mmfp4.marlin_gemm_fp4(xs[4096][:1], ws[1][0], ws[1][1], G)
 
 
-@pytest.mark.parametrize("T,E,k", [(32, 16, 4), (512, 16, 4)])
+@pytest.mark.parametrize("T,E,k", [(32, 16, 4), (512, 16, 4), (1024, 16, 4)])
 def test_moe_mlp_graph_replay(T, E, k):
     import mmfp4
     H, I = 512, 256

@@ -219,10 +219,13 @@ def test_gpu_grouping_api(rng, T, k, E):
 @pytest.mark.parametrize("E,T,k,H,I,i64", [(128, 32, 8, 2048, 768, True), (16, 1, 4, 256, 128, False),
                                           (64, 256, 8, 512, 256, True), (8, 3, 8, 256, 128, False),
                                           (1, 4, 1, 384, 128, False), (128, 5, 8, 2048, 768, False),
-                                          (256, 24, 8, 512, 256, True), (256, 512, 8, 256, 128, False)])
+                                          (256, 24, 8, 512, 256, True), (256, 512, 8, 256, 128, False),
+                                          (64, 1100, 8, 256, 128, True), (32, 2500, 4, 256, 128, False)])
 def test_moe_mlp_one_call_matches_steps(rng, E, T, k, H, I, i64):
     """mm_moe_mlp_fp4 (one library call) is bit-identical to the sort ->
-    grouped GEMM -> grouped GEMM -> combine steps on the same inputs."""
+    grouped GEMM -> grouped GEMM -> combine steps on the same inputs (above
+    8192 assignments the call sorts in blocks of 1024 over two launches, the
+    step path in one block)."""
     import mmfp4
     from mmfp4 import moe_dispatch as md
     g = 128

@@ -74,7 +74,7 @@ def test_shared_expert_and_add(rng):
     assert max_abs_rel(to_np(out2).reshape(T, H), ref + base.astype(np.float32)) <= TOL
 
 
-@pytest.mark.parametrize("T,E,k", [(32, 16, 4), (1, 8, 2), (400, 6, 2), (64, 128, 8)])
+@pytest.mark.parametrize("T,E,k", [(32, 16, 4), (1, 8, 2), (400, 6, 2), (64, 128, 8), (2800, 8, 2)])
 def test_fused_dispatch_shared(rng, T, E, k):
     """Routed experts plus a shared expert in the same grouped launches; the
     (400, 6, 2) case gives every group prefill-sized row counts, and the
@@ -161,7 +161,8 @@ def _proj(rng, K, N, g):
     return ofp4.quantize_fp4(w, g)                 # [K/8, N], [K/g, N]
 
 
-@pytest.mark.parametrize("T,E,k,i64", [(32, 16, 4, False), (512, 8, 2, True), (1, 4, 3, False)])
+@pytest.mark.parametrize("T,E,k,i64", [(32, 16, 4, False), (512, 8, 2, True), (1, 4, 3, False),
+                                        (3000, 8, 2, False)])
 def test_shared_expert_fused_fp4(rng, T, E, k, i64):
     """moe_shared_expert_fused_fp4 (kernels/moe.py:182-329): one projection,
     out = x @ W_sh + sum_j p_j x @ W_e(j), against the fp32 brute force; one
@@ -190,7 +191,7 @@ def test_shared_expert_fused_fp4(rng, T, E, k, i64):
     assert max_abs_rel(to_np(out[0]), ref) <= TOL
 
 
-@pytest.mark.parametrize("T,E,k", [(32, 16, 4), (600, 8, 2)])
+@pytest.mark.parametrize("T,E,k", [(32, 16, 4), (600, 8, 2), (2100, 8, 4)])
 def test_dropped_expert_ids(rng, T, E, k):
     """Ids outside [0, E): the sort places them after every expert's rows in
     index order (the stable argsort of the ids with those mapped to E), and
