@@ -131,9 +131,8 @@ k_skinny(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
   if constexpr (STAGE) {
     static_assert(!INT4 && ACT != SK_MULTI, "row-packed: FP4 product or gate/up pair");
     if constexpr (ROWP <= 2)
-      rowp_wave<MT, NT, SPW, ROWP == 2, false, true>(A, lda, M, tl, N, K, g,
-                                                     blk_st0 + wave * SPW, nrounds, NW * SPW,
-                                                     acc, (char*)red + wave * NT * 8192);
+      rowp_wave<MT, NT, SPW, ROWP == 2>(A, lda, M, tl, N, K, g, blk_st0 + wave * SPW, nrounds,
+                                        NW * SPW, acc, (char*)red + wave * NT * 8192);
     else
       skinny_wave<false, MT, NT, SPW, FL, false, ROWP == 4, false, true>(
           A, lda, nullptr, 1, M, tl, N, K, g, blk_st0 + wave * SPW, nrounds, NW * SPW, acc,
@@ -275,8 +274,9 @@ k_skinny(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
 // 8..15 the second slab against columns 8..15, so D[m][c] + D[8+m][8+c] is
 // row m of the product for column group c.  Half-width tiles double the
 // grid of narrow layers without a K split.
-// ROWP: row-packed FP4 words [N, K/8] (rowp_wave; SPW == 8, K % 512 == 0),
-// scales [N, K/g] when SROW, else [K/g, N].
+// ROWP: row-packed FP4 words [N, K/8] (K % 512 == 0), transposed through
+// LDS into the Marlin operand order (skinny_wave RT); scales [N, K/g] when
+// SROW, else [K/g, N].
 template <bool INT4, int SPW, int NW, int FL, bool SROW = false, bool ROWP = false>
 __global__ void __launch_bounds__(NW * 64)
 k_skinny_dual(const f16* __restrict__ A, const uint32_t* __restrict__ B,

@@ -373,54 +373,45 @@ MM_DEV void skinny_wave(const f16* __restrict__ A, int lda, const int* __restric
 }
 
 // skinny_wave for row-packed FP4 weights (MMFP4 layout): B [N, K/8] words
-// (word (n, kp) holds k = 8kp .. 8kp+7 of column n, LSB-first nibbles) and
-// scales [N, K/g].  The MFMA only needs the activation and weight operands to
-// agree on the k order, so lane (c, q) takes, in a round of SPW 32-k steps
-// (word rows 4*stb .. 4*stb + 4*SPW), the contiguous rows
-// kp(i) = 4*stb + q*SPW + i for step i: each of its four columns is then read
-// as SPW/4 16-byte vectors, the same load count as the Marlin-layout core.
-// (Measured on MI355X, this order beats giving the four lanes q of a column
-// 64 contiguous bytes per load: 4096x28672 at M=1 21.6 vs 25.5 us.)  The
-// eight rows of a lane lie in one scale group (g % 64 == 0), but the lanes q
-// of an MFMA can straddle a group, so weights are scaled before the MFMA
-// (pre-scale, bit-exact fp16 values).  Requires K % 256 == 0 (every round lies
-// inside K) and SPW == 8.
-// DUAL (M <= 8, K % 512 == 0): a step is 64 k and a round 64 word rows; lanes
-// c < 8 take the round's first 32 rows and lanes c >= 8 the next 32, for the
-// 32 columns of lane group c & 7 (the two-slab scheme of skinny_wave).
-
-// STAGE: the round's words are first copied global -> LDS with whole
-// 128-byte lines per column (8 lanes per line, 8 columns per load
-// instruction) into the wave's 8 KiB region per tile (`stage` + 8 KiB * t),
-// then read back in the lanes' layout.  16-byte piece p of LDS column x (the wave's x-th column,
+// (word (n, kp) holds k = 8kp .. 8kp+7 of column n, LSB-first nibbles), used
+// by the split-K grids (the unsplit ones take skinny_wave's RT path).  The
+// MFMA only needs the activation and weight operands to agree on the k
+// order, so lane (c, q) takes, in a round of SPW 32-k steps (word rows
+// 4*stb .. 4*stb + 4*SPW), the contiguous rows kp(i) = 4*stb + q*SPW + i for
+// step i.  The eight rows of a lane lie in one scale group (g % 64 == 0), but
+// the lanes q of an MFMA can straddle a group, so weights are scaled before
+// the MFMA (pre-scale, bit-exact fp16 values).  Requires K % 256 == 0 (every
+// round lies inside K) and SPW == 8.
+// The round's words are first copied global -> LDS with whole 128-byte lines
+// per column (8 lanes per line, 8 columns per load instruction) into the
+// wave's 8 KiB region per tile (`stage` + 8 KiB * t), then read back in the
+// lanes' layout.  16-byte piece p of LDS column x (the wave's x-th column,
 // p = word row / 4 within the round) lives at slot
-//   PPC * x' + (p ^ ((x >> 2) & 7)),  x' = DUAL ? x : x ^ ((x >> 5) & 1),
-// PPC = pieces per column (8, or 16 for DUAL), so the 16 lanes of a read
-// pass (16 columns, one piece each) hit 16 different bank groups.
-template <int MT, int NT, int SPW, bool SG, bool DUAL = false, bool STAGE = false>
+//   8 * x' + (p ^ ((x >> 2) & 7)),  x' = x ^ ((x >> 5) & 1),
+// so the 16 lanes of a read pass (16 columns, one piece each) hit 16
+// different bank groups.
+template <int MT, int NT, int SPW, bool SG>
 MM_DEV void rowp_wave(const f16* __restrict__ A, int lda, int M, const SkTile (&tl)[NT], int N,
                       int K, int g, int st0, int nrounds, int ststride,
-                      f32x4 (&acc)[MT][NT][4], char* stage = nullptr) {
+                      f32x4 (&acc)[MT][NT][4], char* stage) {
   // SG: scales groups-first [K/g, N] (else [N, K/g]).  NT tiles (gate and up
   // matrices of a pair) share the activations.
   static_assert(SPW == 8, "a lane's run of rows is one 64-k piece of a scale group");
   const int lane = threadIdx.x & 63;
   const int c = lane & 15, q = lane >> 4;
-  const int cl = DUAL ? (c & 7) : c, hs = DUAL ? (c >> 3) : 0;
   const int KP = K >> 3, G = K / g;
-  const int nsteps = DUAL ? KP >> 3 : KP >> 2;   // whole steps and rounds (K % 256, K % 512)
+  const int nsteps = KP >> 2;                                   // whole steps and rounds
   uint32_t aoff[MT];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) aoff[mt] = (uint32_t)min(mt * 16 + cl, M - 1) * (uint32_t)lda * 2u;
+  for (int mt = 0; mt < MT; ++mt) aoff[mt] = (uint32_t)min(mt * 16 + c, M - 1) * (uint32_t)lda * 2u;
   uint32_t col[NT];                                             // lane's first column per tile
 #pragma unroll
-  for (int t = 0; t < NT; ++t) col[t] = (uint32_t)min(tl[t].col0 + 4 * cl, N - 4);
+  for (int t = 0; t < NT; ++t) col[t] = (uint32_t)min(tl[t].col0 + 4 * c, N - 4);
   st0 = __builtin_amdgcn_readfirstlane(st0);
   for (int r = 0; r < nrounds; ++r) {
     const int stb = st0 + r * ststride;
     if (stb >= nsteps) break;
-    const uint32_t kp0 = DUAL ? (uint32_t)(8 * stb + 32 * hs + q * SPW)   // lane's first word row
-                              : (uint32_t)(4 * stb + q * SPW);
+    const uint32_t kp0 = (uint32_t)(4 * stb + q * SPW);         // lane's first word row
     const uint32_t gi = kp0 * 8u / (uint32_t)g;
     f16 sc[NT][4];
 #pragma unroll
@@ -435,58 +426,40 @@ MM_DEV void rowp_wave(const f16* __restrict__ A, int lda, int M, const SkTile (&
           sc[t][j] = sanitize_scale(*at_bytes<f16>(tl[t].S, ((col[t] + j) * (uint32_t)G + gi) * 2u));
       }
     }
-    u32x4 w[NT][4][SPW / 4];                                    // [tile][column][4 rows]
-    constexpr int PPC = DUAL ? 16 : 8;                          // 16-byte pieces per column
-    if constexpr (STAGE) {
-      const uint32_t kb = DUAL ? (uint32_t)(8 * stb) : (uint32_t)(4 * stb);   // round's row 0
+    const uint32_t kb = (uint32_t)(4 * stb);                    // round's first word row
 #pragma unroll
-      for (int t = 0; t < NT; ++t)
+    for (int t = 0; t < NT; ++t)
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const int sl = 64 * i + lane;
-          const int xp = sl / PPC, pp = sl % PPC;
-          const int x = DUAL ? xp : (xp ^ ((xp >> 5) & 1));
-          const int p = pp ^ ((x >> 2) & 7);
-          const uint32_t cg = (uint32_t)min(tl[t].col0 + x, N - 1);
-          stage_load16(at_bytes<u32x4>(tl[t].B, (cg * (uint32_t)KP + kb + 4u * p) * 4u),
-                       stage + 8192 * t + 1024 * i);
-        }
-    } else {
-#pragma unroll
-      for (int t = 0; t < NT; ++t)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-          for (int u = 0; u < SPW / 4; ++u)
-            // Plain loads: the two 16-byte pieces of a lane share 128-byte lines
-            // with the neighbouring lanes' pieces, read by the next instruction;
-            // a non-temporal hint made the layer GEMMs ~15% slower (4096x28672
-            // at M=1 21.5 -> 18.4 us without it).
-            w[t][j][u] = *at_bytes<u32x4>(tl[t].B, ((col[t] + j) * (uint32_t)KP + kp0 + 4u * u) * 4u);
-    }
+      for (int i = 0; i < 8; ++i) {
+        const int sl = 64 * i + lane;
+        const int xp = sl / 8, pp = sl % 8;
+        const int x = xp ^ ((xp >> 5) & 1);
+        const int p = pp ^ ((x >> 2) & 7);
+        const uint32_t cg = (uint32_t)min(tl[t].col0 + x, N - 1);
+        stage_load16(at_bytes<u32x4>(tl[t].B, (cg * (uint32_t)KP + kb + 4u * p) * 4u),
+                     stage + 8192 * t + 1024 * i);
+      }
     f16x8 a[SPW][MT];
 #pragma unroll
     for (int i = 0; i < SPW; ++i)
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) a[i][mt] = *at_bytes<f16x8>(A, aoff[mt] + (kp0 + i) * 16u);
-    if constexpr (STAGE) {
-      // Wait for every vector load of the round: the compiler may issue the
-      // activation loads before the copies, so no partial count is safe.
-      __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));   // vmcnt(0)
+    // Wait for every vector load of the round: the compiler may issue the
+    // activation loads before the copies, so no partial count is safe.
+    __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));   // vmcnt(0)
+    u32x4 w[NT][4][SPW / 4];                                    // [tile][column][4 rows]
 #pragma unroll
-      for (int t = 0; t < NT; ++t)
+    for (int t = 0; t < NT; ++t)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int x = (int)(col[t] - (uint32_t)tl[t].col0) + j;
-          const int xp = DUAL ? x : (x ^ ((x >> 5) & 1));
+      for (int j = 0; j < 4; ++j) {
+        const int x = (int)(col[t] - (uint32_t)tl[t].col0) + j;
+        const int xp = x ^ ((x >> 5) & 1);
 #pragma unroll
-          for (int u = 0; u < SPW / 4; ++u) {
-            const int p = DUAL ? 8 * hs + 2 * q + u : 2 * q + u;
-            w[t][j][u] =
-                *(const u32x4*)(stage + 8192 * t + (PPC * xp + (p ^ ((x >> 2) & 7))) * 16);
-          }
+        for (int u = 0; u < SPW / 4; ++u) {
+          const int p = 2 * q + u;
+          w[t][j][u] = *(const u32x4*)(stage + 8192 * t + (8 * xp + (p ^ ((x >> 2) & 7))) * 16);
         }
-    }
+      }
 #pragma unroll
     for (int i = 0; i < SPW; ++i)
 #pragma unroll
