@@ -62,12 +62,23 @@ struct SkMulti {
 // SK_PAIR (NT = 2): tile 0 is columns [n0, n0+64) of (B, S, Z) and tile 1
 // the same columns of (B2, S2, Z2).  Split-K partials are [ksplit][M][PW]
 // fp32 with PW = N, 2N for the pair modes (gate at n, up at N + n), or ntot.
-// ROWP: 0 Marlin-layout weights; row-packed [N, K/8] weights with scales
-// [N, K/g] (1, 4) or [K/g, N] (2, 5), staged through LDS per tile as loaded
-// (1, 2: rowp_wave) or transposed to the Marlin layout (4, 5: skinny_wave
-// RT); 3 Marlin-layout weights with scales [N, K/g].
+// ROWP: 0 Marlin-layout weights; 1, 2 row-packed [N, K/8] weights with
+// scales [N, K/g] (1) or [K/g, N] (2), transposed through LDS into the
+// Marlin operand order (skinny_wave RT); 3 Marlin-layout weights with scales
+// [N, K/g].
+// Row-packed single-tile blocks: the RT staging takes a few registers over
+// the 128 that keep two 8-wave blocks resident per CU; at that limit the
+// flush intervals listed here compile without spills (the others keep the
+// default).  Measured at M=1, 14336 -> 4096 split 7 ways: 11.9 us with the
+// as-loaded staging this replaced, 10.7 us; 4096 -> 28672 15.3 -> 14.5 us.
+template <int ROWP, int NT, int FL>
+constexpr int sk_min_waves() {
+  return NT == 1 && ((ROWP == 2 && (FL == 0 || FL >= 4)) || (ROWP == 1 && (FL == 0 || FL >= 8)))
+             ? 4
+             : 1;
+}
 template <bool INT4, int MT, int NT, int SPW, int NW, int FL, int ACT, int ROWP = 0>
-__global__ void __launch_bounds__(NW * 64)
+__global__ void __launch_bounds__(NW * 64, (sk_min_waves<ROWP, NT, FL>()))
 k_skinny(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
          const f16* __restrict__ S, const f16* __restrict__ Z, const uint32_t* __restrict__ B2,
          const f16* __restrict__ S2, const f16* __restrict__ Z2, f16* __restrict__ C, int ldc,
@@ -78,7 +89,7 @@ k_skinny(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
   constexpr bool ONE = ACT == SK_PLAIN || ACT == SK_MULTI;   // one matrix per block
   // Row-packed weights are staged through 8 KiB of LDS per wave and tile in
   // the main loop; the block reduction reuses the same memory afterwards.
-  constexpr bool STAGE = ROWP == 1 || ROWP == 2 || ROWP == 4 || ROWP == 5;
+  constexpr bool STAGE = ROWP == 1 || ROWP == 2;
   // 9..32 rows, one column tile: each wave's activation slab (16*MT rows x
   // 32*SPW k, 8 KiB) goes through LDS too, when every round lies inside K
   // (measured on MI355X, per Llama layer: M=16 46.6 -> 44.6 us, M=32
@@ -130,14 +141,10 @@ k_skinny(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
                 : (t == 0 ? SkTile{B, S, Z, n0} : SkTile{B2, S2, Z2, n0});
   if constexpr (STAGE) {
     static_assert(!INT4 && ACT != SK_MULTI, "row-packed: FP4 product or gate/up pair");
-    if constexpr (ROWP <= 2)
-      rowp_wave<MT, NT, SPW, ROWP == 2>(A, lda, M, tl, N, K, g, blk_st0 + wave * SPW, nrounds,
-                                        NW * SPW, acc, (char*)red + wave * NT * 8192);
-    else
-      skinny_wave<false, MT, NT, SPW, FL, false, ROWP == 4, false, true>(
-          A, lda, nullptr, 1, M, tl, N, K, g, blk_st0 + wave * SPW, nrounds, NW * SPW, acc,
-          nullptr, (char*)red + wave * NT * 8192);
-    if constexpr (STAGE) __syncthreads();   // every wave is done with its staging area
+    skinny_wave<false, MT, NT, SPW, FL, false, ROWP == 1, false, true>(
+        A, lda, nullptr, 1, M, tl, N, K, g, blk_st0 + wave * SPW, nrounds, NW * SPW, acc,
+        nullptr, (char*)red + wave * NT * 8192);
+    __syncthreads();   // every wave is done with its staging area
   } else if (ASTG && M > 8 && K % (32 * SPW) == 0) {
     skinny_wave<INT4, MT, NT, SPW, FL, false, ROWP == 3, ASTG>(
         A, lda, nullptr, 1, M, tl, N, K, g, blk_st0 + wave * SPW, nrounds, NW * SPW, acc,
@@ -753,8 +760,8 @@ int launch_skinny(const f16* A, int lda, const uint32_t* B, const f16* S, const 
   const int fl = flush_steps(g, SPW);
 #define MM_LAUNCH_SK(FLV, RP)                                                               \
   hipLaunchKernelGGL((k_skinny<INT4, MT, NT, SPW, sk_nw<MT>(), FLV, ACT, RP>), grid,          \
-                     dim3(sk_nw<MT>() * 64), 0, st, A, lda, B, S, Z, B2, S2, Z2, C, ldc, M, N, K, g, p.nrounds, part,       \
-                     counters, mp ? *mp : none)
+                     dim3(sk_nw<MT>() * 64), 0, st, A, lda, B, S, Z, B2, S2, Z2, C, ldc, M, N, \
+                     K, g, p.nrounds, part, counters, mp ? *mp : none)
 #define MM_LAUNCH_SK_FL(RP)                                                                 \
   switch (fl) {                                                                             \
     case 1: MM_LAUNCH_SK(1, RP); break;                                                     \
@@ -763,19 +770,7 @@ int launch_skinny(const f16* A, int lda, const uint32_t* B, const f16* S, const 
     case 8: MM_LAUNCH_SK(8 <= SPW ? 8 : 0, RP); break;                                      \
     default: MM_LAUNCH_SK(0, RP); break;                                                    \
   }
-  // Row-packed weights: the Marlin-layout transpose (RT) path for unsplit
-  // grids; split grids keep the as-loaded staging, whose fewer registers keep
-  // two blocks resident per CU (measured at M=1, 14336 -> 4096: 11.9 against
-  // 13.7 us).
-  if constexpr (ROWP == 1 || ROWP == 2) {
-    if (p.ksplit == 1) {
-      MM_LAUNCH_SK_FL(ROWP + 3)
-    } else {
-      MM_LAUNCH_SK_FL(ROWP)
-    }
-  } else {
-    MM_LAUNCH_SK_FL(ROWP)
-  }
+  MM_LAUNCH_SK_FL(ROWP)
 #undef MM_LAUNCH_SK_FL
 #undef MM_LAUNCH_SK
   MM_CHECK_LAUNCH("gemm(skinny)");

@@ -119,11 +119,6 @@ struct SkTile {
 // addresses are clamped into the matrix so no load is predicated.
 // SROW: scales (and zeros) stored [N, K/g] (the reference MMFP4 kernel's
 // layout) instead of [K/g, N]: the four columns' values are four 2-byte loads.
-// Asynchronous 16-byte copy global -> LDS (lane l writes lds_base + 16 l).
-MM_DEV void stage_load16(const void* src, void* lds_base_uniform) {
-  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds_base_uniform,
-                                   16, 0, 0);
-}
 
 // ASTG (16*MT rows x SPW steps = 8 KiB, no row map, every round inside K):
 // each round's activation slab -- 16*MT rows x 32*SPW k (DUAL: 8 rows x
@@ -369,109 +364,6 @@ MM_DEV void skinny_wave(const f16* __restrict__ A, int lda, const int* __restric
           }
       }
     }
-  }
-}
-
-// skinny_wave for row-packed FP4 weights (MMFP4 layout): B [N, K/8] words
-// (word (n, kp) holds k = 8kp .. 8kp+7 of column n, LSB-first nibbles), used
-// by the split-K grids (the unsplit ones take skinny_wave's RT path).  The
-// MFMA only needs the activation and weight operands to agree on the k
-// order, so lane (c, q) takes, in a round of SPW 32-k steps (word rows
-// 4*stb .. 4*stb + 4*SPW), the contiguous rows kp(i) = 4*stb + q*SPW + i for
-// step i.  The eight rows of a lane lie in one scale group (g % 64 == 0), but
-// the lanes q of an MFMA can straddle a group, so weights are scaled before
-// the MFMA (pre-scale, bit-exact fp16 values).  Requires K % 256 == 0 (every
-// round lies inside K) and SPW == 8.
-// The round's words are first copied global -> LDS with whole 128-byte lines
-// per column (8 lanes per line, 8 columns per load instruction) into the
-// wave's 8 KiB region per tile (`stage` + 8 KiB * t), then read back in the
-// lanes' layout.  16-byte piece p of LDS column x (the wave's x-th column,
-// p = word row / 4 within the round) lives at slot
-//   8 * x' + (p ^ ((x >> 2) & 7)),  x' = x ^ ((x >> 5) & 1),
-// so the 16 lanes of a read pass (16 columns, one piece each) hit 16
-// different bank groups.
-template <int MT, int NT, int SPW, bool SG>
-MM_DEV void rowp_wave(const f16* __restrict__ A, int lda, int M, const SkTile (&tl)[NT], int N,
-                      int K, int g, int st0, int nrounds, int ststride,
-                      f32x4 (&acc)[MT][NT][4], char* stage) {
-  // SG: scales groups-first [K/g, N] (else [N, K/g]).  NT tiles (gate and up
-  // matrices of a pair) share the activations.
-  static_assert(SPW == 8, "a lane's run of rows is one 64-k piece of a scale group");
-  const int lane = threadIdx.x & 63;
-  const int c = lane & 15, q = lane >> 4;
-  const int KP = K >> 3, G = K / g;
-  const int nsteps = KP >> 2;                                   // whole steps and rounds
-  uint32_t aoff[MT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) aoff[mt] = (uint32_t)min(mt * 16 + c, M - 1) * (uint32_t)lda * 2u;
-  uint32_t col[NT];                                             // lane's first column per tile
-#pragma unroll
-  for (int t = 0; t < NT; ++t) col[t] = (uint32_t)min(tl[t].col0 + 4 * c, N - 4);
-  st0 = __builtin_amdgcn_readfirstlane(st0);
-  for (int r = 0; r < nrounds; ++r) {
-    const int stb = st0 + r * ststride;
-    if (stb >= nsteps) break;
-    const uint32_t kp0 = (uint32_t)(4 * stb + q * SPW);         // lane's first word row
-    const uint32_t gi = kp0 * 8u / (uint32_t)g;
-    f16 sc[NT][4];
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      if constexpr (SG) {
-        const f16x4 s4 = *at_bytes<f16x4>(tl[t].S, (gi * (uint32_t)N + col[t]) * 2u);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) sc[t][j] = sanitize_scale(s4[j]);
-      } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          sc[t][j] = sanitize_scale(*at_bytes<f16>(tl[t].S, ((col[t] + j) * (uint32_t)G + gi) * 2u));
-      }
-    }
-    const uint32_t kb = (uint32_t)(4 * stb);                    // round's first word row
-#pragma unroll
-    for (int t = 0; t < NT; ++t)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int sl = 64 * i + lane;
-        const int xp = sl / 8, pp = sl % 8;
-        const int x = xp ^ ((xp >> 5) & 1);
-        const int p = pp ^ ((x >> 2) & 7);
-        const uint32_t cg = (uint32_t)min(tl[t].col0 + x, N - 1);
-        stage_load16(at_bytes<u32x4>(tl[t].B, (cg * (uint32_t)KP + kb + 4u * p) * 4u),
-                     stage + 8192 * t + 1024 * i);
-      }
-    f16x8 a[SPW][MT];
-#pragma unroll
-    for (int i = 0; i < SPW; ++i)
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) a[i][mt] = *at_bytes<f16x8>(A, aoff[mt] + (kp0 + i) * 16u);
-    // Wait for every vector load of the round: the compiler may issue the
-    // activation loads before the copies, so no partial count is safe.
-    __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));   // vmcnt(0)
-    u32x4 w[NT][4][SPW / 4];                                    // [tile][column][4 rows]
-#pragma unroll
-    for (int t = 0; t < NT; ++t)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int x = (int)(col[t] - (uint32_t)tl[t].col0) + j;
-        const int xp = x ^ ((x >> 5) & 1);
-#pragma unroll
-        for (int u = 0; u < SPW / 4; ++u) {
-          const int p = 2 * q + u;
-          w[t][j][u] = *(const u32x4*)(stage + 8192 * t + (8 * xp + (p ^ ((x >> 2) & 7))) * 16);
-        }
-      }
-#pragma unroll
-    for (int i = 0; i < SPW; ++i)
-#pragma unroll
-      for (int t = 0; t < NT; ++t)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const f16x8 b = WordDq<false>::run(w[t][j][i >> 2][i & 3], sc[t][j], (f16)0);
-#pragma unroll
-          for (int mt = 0; mt < MT; ++mt)
-            acc[mt][t][j] =
-                __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i][mt], b, acc[mt][t][j], 0, 0, 0);
-        }
   }
 }
 
