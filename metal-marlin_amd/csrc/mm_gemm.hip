@@ -1146,15 +1146,15 @@ extern "C" int mm_fp4_gemm_rowpacked(const uint16_t* A, const uint32_t* B, const
   MM_CHECK_ARG(scales_layout == 0 || scales_layout == 1,
                "%s: scales_layout=%d must be 0 ([K/g, N]) or 1 ([N, K/g])", who, scales_layout);
   MM_CHECK_ARG(M >= 0 && N > 0 && K > 0, "%s: bad shape M=%d N=%d K=%d", who, M, N, K);
-  MM_CHECK_ARG(M <= 16 || scales_layout == 0,
-               "%s: M=%d: above 16 rows the scales must be [K/g, N] (scales_layout 0)", who, M);
-  MM_CHECK_ARG(M <= 16 || N % 8 == 0, "%s: N=%d must be divisible by 8 for M > 16", who, N);
+  MM_CHECK_ARG(M <= 32 || scales_layout == 0,
+               "%s: M=%d: above 32 rows the scales must be [K/g, N] (scales_layout 0)", who, M);
+  MM_CHECK_ARG(M <= 32 || N % 8 == 0, "%s: N=%d must be divisible by 8 for M > 32", who, N);
   MM_CHECK_ARG(K % 256 == 0, "%s: K=%d must be divisible by 256", who, K);
   MM_CHECK_ARG(g > 0 && g % 64 == 0 && K % g == 0,
                "%s: group_size=%d must be a multiple of 64 dividing K=%d", who, g, K);
   MM_CHECK_ARG(N % 4 == 0, "%s: N=%d must be divisible by 4", who, N);
-  MM_CHECK_ARG(M > 16 || (size_t)N * (size_t)(K / 8) * 4 < ((size_t)1 << 32),
-               "%s: the packed weights must be under 4 GiB at M <= 16", who);
+  MM_CHECK_ARG(M > 32 || (size_t)N * (size_t)(K / 8) * 4 < ((size_t)1 << 32),
+               "%s: the packed weights must be under 4 GiB at M <= 32", who);
   // [K/g, N] scales are read as 4 adjacent columns (8 bytes) per lane.
   const uintptr_t salign = scales_layout == 0 ? 7 : 1;
   MM_CHECK_ARG(((uintptr_t)A & 15) == 0 && ((uintptr_t)B & 15) == 0 &&
@@ -1163,7 +1163,17 @@ extern "C" int mm_fp4_gemm_rowpacked(const uint16_t* A, const uint32_t* B, const
                "scales 8-byte)", who);
   if (M == 0) return 0;
   hipStream_t st = (hipStream_t)stream;
-  if (M > 16) {
+  if (M > 16 && M <= 32) {
+    // Two-row-block decode kernel, as the Marlin-layout path at these sizes.
+    if (scales_layout == 1)
+      return launch_skinny<false, 2, SK_PLAIN, 1>((const f16*)A, K, B, (const f16*)S, nullptr,
+                                                  nullptr, nullptr, nullptr, (f16*)C, N, M, N,
+                                                  K, g, ws, ws_bytes, st);
+    return launch_skinny<false, 2, SK_PLAIN, 2>((const f16*)A, K, B, (const f16*)S, nullptr,
+                                                nullptr, nullptr, nullptr, (f16*)C, N, M, N, K,
+                                                g, ws, ws_bytes, st);
+  }
+  if (M > 32) {
     // Pipelined prefill kernel reading the row-packed words in place.
     const PrefillPlan p = plan_prefill(M, N, K);
     float* part = nullptr;
@@ -1266,15 +1276,26 @@ extern "C" int mm_fp4_gate_up_rowpacked(const uint16_t* A, const uint32_t* Bg, c
   MM_CHECK_ARG(g > 0 && g % 64 == 0 && K % g == 0,
                "%s: group_size=%d must be a multiple of 64 dividing K=%d", who, g, K);
   MM_CHECK_ARG(N % 8 == 0, "%s: N=%d must be divisible by 8", who, N);
-  MM_CHECK_ARG(M > 16 || (size_t)N * (size_t)(K / 8) * 4 < ((size_t)1 << 32),
-               "%s: each packed matrix must be under 4 GiB at M <= 16", who);
+  MM_CHECK_ARG(M > 32 || (size_t)N * (size_t)(K / 8) * 4 < ((size_t)1 << 32),
+               "%s: each packed matrix must be under 4 GiB at M <= 32", who);
   const uintptr_t a16 = (uintptr_t)A | (uintptr_t)Bg | (uintptr_t)Bu;
   MM_CHECK_ARG((a16 & 15) == 0 && (((uintptr_t)Sg | (uintptr_t)Su) & 7) == 0 &&
                    ((uintptr_t)C & 7) == 0,
                "%s: A and the packed weights must be 16-byte aligned, scales and C 8-byte", who);
   if (M == 0) return 0;
   const int ldc = act ? N : 2 * N;
-  if (M > 16) {
+  if (M > 16 && M <= 32) {
+    // Two-row-block decode kernel over both matrices, as the Marlin-layout
+    // pair at these sizes.
+    if (act)
+      return launch_skinny<false, 2, SK_SWIGLU, 2>((const f16*)A, K, Bg, (const f16*)Sg, nullptr,
+                                                   Bu, (const f16*)Su, nullptr, (f16*)C, ldc, M,
+                                                   N, K, g, ws, ws_bytes, (hipStream_t)stream);
+    return launch_skinny<false, 2, SK_PAIR, 2>((const f16*)A, K, Bg, (const f16*)Sg, nullptr, Bu,
+                                               (const f16*)Su, nullptr, (f16*)C, ldc, M, N, K, g,
+                                               ws, ws_bytes, (hipStream_t)stream);
+  }
+  if (M > 32) {
     // Pipelined prefill kernel reading both row-packed matrices in place;
     // split and workspace as the unfused [K, 2N] product.
     const PrefillPlan p = plan_prefill(M, 2 * N, K);

@@ -129,10 +129,10 @@ struct SkTile {
 // the round) lives at slot PPR * r + (p ^ sw(r)), PPR = 4*SPW (DUAL: 64)
 // pieces per row, sw(r) = r % 16 (DUAL: bits 0, 1, 3 from r's bits 0, 1, 2),
 // so the 16 lanes of a read pass hit 16 bank groups.
-// RT (row-packed weights [N, K/8], FP4, SPW == 8, every round inside K):
-// each round's words -- 32 word rows x 64 columns (DUAL: 64 x 32), 8 KiB
-// per tile -- are loaded with whole lines (a column's 128 or 256 contiguous
-// bytes, 8 or 16 lanes per column) and written to the wave's LDS region
+// RT (row-packed weights [N, K/8], FP4, SPW == 8 (or 4 without DUAL), every
+// round inside K): each round's words -- 4*SPW word rows x 64 columns (DUAL:
+// 64 x 32), 8 KiB per tile at SPW 8 -- are loaded with whole row segments (a
+// column's 4*SPW*4 contiguous bytes, SPW or 16 lanes per column) and written to the wave's LDS region
 // `rstage` transposed to the Marlin layout [word row][column], so the rest
 // of the round (the k order, the post-scale decode, the MFMAs) is the
 // Marlin-layout path's.  Word (row r, column x) lives at dword
@@ -146,7 +146,8 @@ MM_DEV void skinny_wave(const f16* __restrict__ A, int lda, const int* __restric
                         int rowdiv, int M, const SkTile (&tl)[NT], int N, int K, int g,
                         int st0, int nrounds, int ststride, f32x4 (&acc)[MT][NT][4],
                         char* astage = nullptr, char* rstage = nullptr) {
-  static_assert(!RT || (!INT4 && SPW == 8 && !ASTG), "row-packed staging: FP4, 8 steps");
+  static_assert(!RT || (!INT4 && (SPW == 8 || (SPW == 4 && !DUAL)) && !ASTG),
+                "row-packed staging: FP4, 8 steps (4 for single-slab blocks)");
   static_assert(FL == 0 || (SPW % FL == 0), "flush interval must divide the round");
   static_assert(!ASTG || (DUAL ? 8 * 64 : 16 * MT * 4 * SPW) == 512,
                 "activation staging: an 8 KiB slab per wave");
@@ -208,14 +209,16 @@ MM_DEV void skinny_wave(const f16* __restrict__ A, int lda, const int* __restric
       }
     }
     constexpr int RW = DUAL ? 32 : 64;       // RT: columns per tile (dwords per LDS row)
-    constexpr int RPC = DUAL ? 16 : 8;       // RT: 16-byte pieces per column per round
-    u32x4 wp[RT ? NT : 1][RT ? 8 : 1];       // RT: this lane's 8 loaded pieces per tile
+    constexpr int RPC = SLAB * SPW;          // RT: 16-byte pieces per column per round
+    constexpr int RTB = RW * RPC * 16;       // RT: staging bytes per tile
+    constexpr int RNI = RW * RPC / 64;       // RT: load instructions per tile
+    u32x4 wp[RT ? NT : 1][RT ? RNI : 1];     // RT: this lane's loaded pieces per tile
     if constexpr (RT) {
       const uint32_t kb = (uint32_t)(4 * SLAB * stb);   // round's first word row
 #pragma unroll
       for (int t = 0; t < NT; ++t)
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < RNI; ++i) {
           const int sl = 64 * i + lane;
           const int x = sl / RPC, p = sl % RPC;
           const uint32_t cg = (uint32_t)min(tl[t].col0 + x, N - 1);
@@ -243,13 +246,13 @@ MM_DEV void skinny_wave(const f16* __restrict__ A, int lda, const int* __restric
 #pragma unroll
       for (int t = 0; t < NT; ++t)
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < RNI; ++i) {
           const int sl = 64 * i + lane;
           const int x = sl / RPC, p = sl % RPC;
 #pragma unroll
           for (int k = 0; k < 4; ++k) {
             const int row = 4 * p + k;
-            *(uint32_t*)(rstage + 8192 * t + (row * RW + (x ^ (4 * ((row >> 2) & 7)))) * 4) =
+            *(uint32_t*)(rstage + RTB * t + (row * RW + (x ^ (4 * ((row >> 2) & 7)))) * 4) =
                 wp[t][i][k];
           }
         }
@@ -259,7 +262,7 @@ MM_DEV void skinny_wave(const f16* __restrict__ A, int lda, const int* __restric
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
           const int x0 = (int)(coff[t] - (uint32_t)tl[t].col0);
-          w[i][t] = *(const u32x4*)(rstage + 8192 * t +
+          w[i][t] = *(const u32x4*)(rstage + RTB * t +
                                    (row * RW + (x0 ^ (4 * ((row >> 2) & 7)))) * 4);
         }
       }

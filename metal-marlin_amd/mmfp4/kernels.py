@@ -129,7 +129,7 @@ def marlin_gemm_fp4(A: torch.Tensor, B_packed: torch.Tensor, scales: torch.Tenso
 def rowpacked_gemm_supported(M: int, N: int, K: int, group_size: int) -> bool:
     """Shapes mm_fp4_gemm_rowpacked takes (row-packed words read in place)."""
     return (M > 0 and K % 256 == 0 and group_size > 0 and group_size % 64 == 0
-            and K % group_size == 0 and N % (4 if M <= 16 else 8) == 0)
+            and K % group_size == 0 and N % (4 if M <= 32 else 8) == 0)
 
 
 def _scales_layout(scales: torch.Tensor, N: int, n_groups: int, name: str = "scales") -> int:
@@ -148,7 +148,7 @@ def mmfp4_gemm_rowpacked(A: torch.Tensor, B_rows: torch.Tensor, scales: torch.Te
                          group_size: int = 128) -> torch.Tensor:
     """A [M, K] @ dequant(B_rows)^T with row-packed weights read in place:
     B_rows [N, K/8] words, scales [K/group_size, N] (the layer's canonical
-    layout) or [N, K/group_size] (layers/mmfp4_linear.py:549-598).  M <= 16
+    layout) or [N, K/group_size] (layers/mmfp4_linear.py:549-598).  M <= 32
     runs the decode kernels; larger M the pipelined prefill kernel, which
     reads the words in place too but takes [K/group_size, N] scales (the
     other layout is transposed here, K/group_size x N halves)."""
@@ -163,7 +163,7 @@ def mmfp4_gemm_rowpacked(A: torch.Tensor, B_rows: torch.Tensor, scales: torch.Te
     a = _half(A)
     b = _packed(B_rows)
     s = _half(scales)
-    if M > 16 and layout == 1:
+    if M > 32 and layout == 1:
         s, layout = s.t().contiguous(), 0
     out = torch.empty((M, N), dtype=torch.float16, device=dev)
     ws = _lib.workspace(dev, int(_lib.load().mm_gemm_workspace_bytes(M, N, K)))
@@ -241,7 +241,7 @@ def mmfp4_fused_gate_up(x: torch.Tensor, gate_packed: torch.Tensor, gate_scales:
     gate_packed / up_packed row-packed [N, K/8] uint32, scales [K/group_size, N].
     With K % 256 == 0, group size % 64 == 0 and N % 8 == 0 the row-packed
     words are read in place at every M (mm_fp4_gate_up_rowpacked: the decode
-    kernel up to 16 rows, the pipelined prefill kernel above); other shapes
+    kernel up to 32 rows, the pipelined prefill kernel above); other shapes
     are transposed to the Marlin layout on the device for each call (as the
     reference's own M < 64 path does); callers that keep the Marlin layout
     call `mmfp4_fused_gate_up_marlin`.

@@ -90,11 +90,11 @@ def test_new_entry_points_validate():
     with pytest.raises(ValueError, match="scales_layout"):
         _lib.call("mm_fp4_gemm_rowpacked", None, None, None, None, 1, 64, 256, 64, 2, None, 0,
                   None)
-    with pytest.raises(ValueError, match="scales_layout 0"):      # M > 16, [N, K/g] scales
-        _lib.call("mm_fp4_gemm_rowpacked", None, None, None, None, 17, 64, 256, 64, 1, None, 0,
+    with pytest.raises(ValueError, match="scales_layout 0"):      # M > 32, [N, K/g] scales
+        _lib.call("mm_fp4_gemm_rowpacked", None, None, None, None, 33, 64, 256, 64, 1, None, 0,
                   None)
-    with pytest.raises(ValueError, match="divisible by 8"):       # M > 16, N % 8 != 0
-        _lib.call("mm_fp4_gemm_rowpacked", None, None, None, None, 17, 60, 256, 64, 0, None, 0,
+    with pytest.raises(ValueError, match="divisible by 8"):       # M > 32, N % 8 != 0
+        _lib.call("mm_fp4_gemm_rowpacked", None, None, None, None, 33, 60, 256, 64, 0, None, 0,
                   None)
     with pytest.raises(ValueError, match="built-in scratch"):
         _lib.call("mm_fp4_gemm_noalloc", None, None, None, None, 256, 4096, 4096, 128, None)

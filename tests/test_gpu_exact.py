@@ -110,14 +110,16 @@ def test_u4_gemm_bit_exact(rng, M, K, N, g, family):
 
 @pytest.mark.parametrize("M,K,N,g", [(1, 4096, 6144, 128), (1, 14336, 4096, 128),
                                      (12, 4096, 4096, 64), (4, 4096, 28672, 128),
-                                     (17, 4096, 4096, 128), (64, 4096, 1024, 128),
+                                     (17, 4096, 4096, 128), (32, 14336, 4096, 128),
+                                     (24, 4096, 28672, 64), (33, 4096, 1024, 128),
+                                     (64, 4096, 1024, 128),
                                      (128, 14336, 4096, 128), (300, 2048, 1000, 64),
                                      (512, 4096, 14336, 128)])
 def test_rowpacked_and_mmfp4_bit_exact(rng, M, K, N, g):
     """Row-packed words (both scale layouts) and Marlin words with [N, K/g]
-    scales: the two-slab and skinny in-place variants (M <= 16) and the
-    pipelined prefill kernel on row-packed words (M > 16: 64-, 128- and
-    256-row tiles, split-K, ragged N)."""
+    scales: the two-slab and skinny in-place variants (M <= 32, one and two
+    row blocks, split-K) and the pipelined prefill kernel on row-packed words
+    (M > 32: 64-, 128- and 256-row tiles, split-K, ragged N)."""
     import mmfp4
     packed, scales = _exact_fp4(rng, K, N, g)
     a = _acts(rng, M, K)

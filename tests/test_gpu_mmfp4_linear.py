@@ -103,10 +103,10 @@ def test_rowpacked_gemm_in_place(M, K, N, g):
 
 def test_rowpacked_gemm_refuses_unsupported_shapes():
     import mmfp4
-    a = torch.zeros((17, 512), dtype=torch.float16, device="cuda")
+    a = torch.zeros((33, 512), dtype=torch.float16, device="cuda")
     rows = torch.zeros((64, 64), dtype=torch.int32, device="cuda")
     s = torch.ones((64, 4), dtype=torch.float16, device="cuda")
-    with pytest.raises(ValueError):                          # M > 16 needs N % 8 == 0
+    with pytest.raises(ValueError):                          # M > 32 needs N % 8 == 0
         mmfp4.mmfp4_gemm_rowpacked(a, rows[:60], s[:60], 128)
     with pytest.raises(ValueError):                          # K % 256 != 0
         mmfp4.mmfp4_gemm_rowpacked(a[:1, :384], rows[:, :48], s[:, :3], 128)
