@@ -678,12 +678,14 @@ k_splitk_reduce(const float* __restrict__ part, int ks, int M, int N, f16* __res
 #define MM_SK_MAXBLOCKS 2048
 template <int MT> constexpr int sk_nw() { return MT == 1 ? MM_SK_NW1 : MM_SK_NW2; }
 template <int MT> constexpr int sk_spw() { return MT == 1 ? MM_SK_SPW1 : MM_SK_SPW2; }
-// The gate/up pair (two column tiles per wave) at M <= 16 takes half-length
-// slabs: twice the blocks along K for the same bytes.  Measured on MI355X,
-// 4096 -> 2 x 14336, M=1: 13.7 -> 13.0 us; M=8 and M=16 within 1%.
+// The Marlin-layout gate/up pair (two column tiles per wave) at M <= 16 takes
+// half-length slabs: twice the blocks along K for the same bytes.  Measured
+// on MI355X, 4096 -> 2 x 14336, M=1: 13.7 -> 13.0 us; M=8 and M=16 within 1%.
+// The row-packed pair keeps 8 steps (4 steps: M=1 16.7 -> 18.5 us).
 #define MM_SK_PAIR_SPW1 4
-template <int MT, int ACT> constexpr int sk_spw_act() {
-  return (ACT == SK_SWIGLU || ACT == SK_PAIR) && MT == 1 ? MM_SK_PAIR_SPW1 : sk_spw<MT>();
+template <int MT, int ACT, int ROWP> constexpr int sk_spw_act() {
+  return (ACT == SK_SWIGLU || ACT == SK_PAIR) && MT == 1 && ROWP == 0 ? MM_SK_PAIR_SPW1
+                                                                      : sk_spw<MT>();
 }
 // One 64-column virtual-tile quad per block: more column tiles means fewer
 // K splits (less partial-sum traffic) for the same parallelism.
@@ -748,7 +750,7 @@ int launch_skinny(const f16* A, int lda, const uint32_t* B, const f16* S, const 
                   int N, int K, int g, void* ws, size_t ws_bytes, hipStream_t st,
                   const SkMulti* mp = nullptr) {
   const int PW = ACT == SK_PLAIN || ACT == SK_MULTI ? N : 2 * N;
-  constexpr int SPW = sk_spw_act<MT, ACT>();
+  constexpr int SPW = sk_spw_act<MT, ACT, ROWP>();
   const SkinnyPlan p = plan_skinny(M, PW, K, SPW);
   constexpr int NT =
       ACT == SK_PLAIN || ACT == SK_MULTI ? (ROWP == 1 || ROWP == 2 ? MM_ROWP_TILES : sk_nt<MT>())
