@@ -56,7 +56,8 @@ def test_gate_up_rowpacked_vs_oracle(rng, M, K, N, g):
     """mmfp4_fused_gate_up on row-packed [N, K/8] weights (the reference's
     documented layout) against the numpy oracle: read in place by the decode
     kernel (M <= 16) and the pipelined prefill kernel (M > 16, including a
-    ragged N and a split-K grid); K % 256 != 0 is transposed per call."""
+    ragged N, a split-K grid and K % 256 != 0); K % 256 != 0 at M <= 32 is
+    transposed per call."""
     import mmfp4
     wg = rng.normal(0, 0.02, (N, K)).astype(np.float16)
     wu = rng.normal(0, 0.02, (N, K)).astype(np.float16)
