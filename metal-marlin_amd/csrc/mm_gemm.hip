@@ -1161,7 +1161,6 @@ extern "C" int mm_fp4_gemm_rowpacked(const uint16_t* A, const uint32_t* B, const
   MM_CHECK_ARG(M <= 32 || scales_layout == 0,
                "%s: M=%d: above 32 rows the scales must be [K/g, N] (scales_layout 0)", who, M);
   MM_CHECK_ARG(M <= 32 || N % 8 == 0, "%s: N=%d must be divisible by 8 for M > 32", who, N);
-  MM_CHECK_ARG(M > 32 || K % 256 == 0, "%s: K=%d must be divisible by 256 for M <= 32", who, K);
   MM_CHECK_ARG(g > 0 && g % 64 == 0 && K % g == 0,
                "%s: group_size=%d must be a multiple of 64 dividing K=%d", who, g, K);
   MM_CHECK_ARG(N % 4 == 0, "%s: N=%d must be divisible by 4", who, N);
@@ -1284,7 +1283,6 @@ extern "C" int mm_fp4_gate_up_rowpacked(const uint16_t* A, const uint32_t* Bg, c
   const char* who = "mm_fp4_gate_up_rowpacked";
   MM_CHECK_ARG(act == 0 || act == 1, "%s: act=%d must be 0 or 1", who, act);
   MM_CHECK_ARG(M >= 0 && N > 0 && K > 0, "%s: bad shape M=%d N=%d K=%d", who, M, N, K);
-  MM_CHECK_ARG(M > 32 || K % 256 == 0, "%s: K=%d must be divisible by 256 for M <= 32", who, K);
   MM_CHECK_ARG(g > 0 && g % 64 == 0 && K % g == 0,
                "%s: group_size=%d must be a multiple of 64 dividing K=%d", who, g, K);
   MM_CHECK_ARG(N % 8 == 0, "%s: N=%d must be divisible by 8", who, N);

@@ -214,6 +214,9 @@ MM_DEV void skinny_wave(const f16* __restrict__ A, int lda, const int* __restric
     constexpr int RNI = RW * RPC / 64;       // RT: load instructions per tile
     u32x4 wp[RT ? NT : 1][RT ? RNI : 1];     // RT: this lane's loaded pieces per tile
     if constexpr (RT) {
+      // A round overhanging K re-reads the column's last piece (its steps
+      // are zeroed through the activation operand below), so every load stays
+      // inside the column's KP words (KP % 4 == 0).
       const uint32_t kb = (uint32_t)(4 * SLAB * stb);   // round's first word row
 #pragma unroll
       for (int t = 0; t < NT; ++t)
@@ -222,8 +225,9 @@ MM_DEV void skinny_wave(const f16* __restrict__ A, int lda, const int* __restric
           const int sl = 64 * i + lane;
           const int x = sl / RPC, p = sl % RPC;
           const uint32_t cg = (uint32_t)min(tl[t].col0 + x, N - 1);
+          const uint32_t kw = min(kb + 4u * (uint32_t)p, (uint32_t)KP - 4u);
           wp[t][i] = __builtin_nontemporal_load(
-              at_bytes<u32x4>(tl[t].B, (cg * (uint32_t)KP + kb + 4u * (uint32_t)p) * 4u));
+              at_bytes<u32x4>(tl[t].B, (cg * (uint32_t)KP + kw) * 4u));
         }
     }
 #pragma unroll

@@ -4,8 +4,7 @@ mmfp4_linear.py:414-478, 549-598, 600-960).
 Row-packed means `packed_weights` uint32 [out_features, in_features // 8],
 word (n, j) holding inputs 8j..8j+7 of output n (LSB first); scales are
 [n_groups, out_features] or [out_features, n_groups].  When the group size
-is a multiple of 64 (and K % 256 == 0 up to 32 rows, out_features % 8 == 0
-above), both the functional `mmfp4_gemm` and `MMFP4Linear` read the
+is a multiple of 64 (and out_features % 8 == 0 above 32 rows), both the functional `mmfp4_gemm` and `MMFP4Linear` read the
 row-packed words in place at every M (mm_fp4_gemm_rowpacked: the decode
 kernels up to 32 rows, the pipelined prefill kernel above), so the layer
 holds one copy of its weights.  Other shapes run the Marlin-layout kernels

@@ -115,12 +115,15 @@ def test_u4_gemm_bit_exact(rng, M, K, N, g, family):
                                      (64, 4096, 1024, 128),
                                      (128, 14336, 4096, 128), (300, 2048, 1000, 64),
                                      (512, 4096, 14336, 128), (48, 2880, 1024, 64),
-                                     (100, 1408, 528, 64)])
+                                     (100, 1408, 528, 64), (1, 2880, 1024, 64),
+                                     (5, 896, 4864, 128), (13, 1408, 2048, 64),
+                                     (24, 2880, 516, 64), (32, 1408, 8192, 128)])
 def test_rowpacked_and_mmfp4_bit_exact(rng, M, K, N, g):
     """Row-packed words (both scale layouts) and Marlin words with [N, K/g]
     scales: the two-slab and skinny in-place variants (M <= 32, one and two
     row blocks, split-K) and the pipelined prefill kernel on row-packed words
-    (M > 32: 64-, 128- and 256-row tiles, split-K, ragged N, K % 256 != 0)."""
+    (M > 32: 64-, 128- and 256-row tiles, split-K, ragged N), and K % 256 != 0
+    (rounds overhanging K) on both."""
     import mmfp4
     packed, scales = _exact_fp4(rng, K, N, g)
     a = _acts(rng, M, K)
