@@ -76,9 +76,9 @@ int mm_fp4_gemm(const uint16_t* A, const uint32_t* B, const uint16_t* scales, ui
  * B [N, K/8] uint32 (word (n, kp) holds k = 8kp .. 8kp+7 of row n), scales
  * fp16 [K/g, N] (scales_layout = 0, the layer's canonical [n_groups, N]) or
  * [N, K/g] (scales_layout = 1, the transposed layout the layer also accepts,
- * metal_marlin/layers/mmfp4_linear.py:53-86).  g % 64 == 0, N % 4 == 0;
- * M <= 32 runs the decode kernels, larger M the pipelined
- * prefill kernel, which needs N % 8 == 0 and scales_layout 0.  Weights and scales are
+ * metal_marlin/layers/mmfp4_linear.py:53-86).  N % 4 == 0; M <= 32 runs the
+ * decode kernels (g % 32 == 0), larger M the pipelined prefill kernel, which
+ * needs g % 64 == 0, N % 8 == 0 and scales_layout 0.  Weights and scales are
  * read in place at every M (no transpose).  Workspace as
  * mm_gemm_workspace_bytes(M, N, K).  Replaces
  * metal_marlin/layers/mmfp4_linear.py:549-598 (mmfp4_gemm), which transposes
@@ -136,8 +136,8 @@ int mm_fp4_gemm_mmfp4(const uint16_t* A, const uint32_t* B, const uint16_t* scal
 
 /* mm_fp4_gate_up for row-packed (MMFP4) gate and up matrices read in place:
  * Bg, Bu [N, K/8] uint32, scales Sg, Su fp16 [K/g, N]; act as mm_fp4_gate_up.
- * g % 64 == 0, N % 8 == 0; M <= 32 runs the decode kernel, larger
- * M the pipelined prefill kernel, both reading the words in place.
+ * N % 8 == 0; M <= 32 runs the decode kernel (g % 32 == 0), larger M the
+ * pipelined prefill kernel (g % 64 == 0), both reading the words in place.
  * Workspace: mm_gemm_workspace_bytes(M, 2N, K).  Replaces
  * metal_marlin/kernels_core.py:4762-4774 (mmfp4_fused_gate_up) ->
  * MetalKernels.mmfp4_fused_gate_up :4269-4408 on its row-packed inputs,

@@ -1161,8 +1161,11 @@ extern "C" int mm_fp4_gemm_rowpacked(const uint16_t* A, const uint32_t* B, const
   MM_CHECK_ARG(M <= 32 || scales_layout == 0,
                "%s: M=%d: above 32 rows the scales must be [K/g, N] (scales_layout 0)", who, M);
   MM_CHECK_ARG(M <= 32 || N % 8 == 0, "%s: N=%d must be divisible by 8 for M > 32", who, N);
-  MM_CHECK_ARG(g > 0 && g % 64 == 0 && K % g == 0,
-               "%s: group_size=%d must be a multiple of 64 dividing K=%d", who, g, K);
+  // The decode kernels take any multiple of 32 (one scale group per 32-k step
+  // or more); the pipelined prefill kernel stages 64-k chunks of one group.
+  MM_CHECK_ARG(g > 0 && g % (M <= 32 ? 32 : 64) == 0 && K % g == 0,
+               "%s: group_size=%d must be a multiple of %d dividing K=%d", who, g,
+               M <= 32 ? 32 : 64, K);
   MM_CHECK_ARG(N % 4 == 0, "%s: N=%d must be divisible by 4", who, N);
   MM_CHECK_ARG(M > 32 || (size_t)N * (size_t)(K / 8) * 4 < ((size_t)1 << 32),
                "%s: the packed weights must be under 4 GiB at M <= 32", who);
@@ -1283,8 +1286,11 @@ extern "C" int mm_fp4_gate_up_rowpacked(const uint16_t* A, const uint32_t* Bg, c
   const char* who = "mm_fp4_gate_up_rowpacked";
   MM_CHECK_ARG(act == 0 || act == 1, "%s: act=%d must be 0 or 1", who, act);
   MM_CHECK_ARG(M >= 0 && N > 0 && K > 0, "%s: bad shape M=%d N=%d K=%d", who, M, N, K);
-  MM_CHECK_ARG(g > 0 && g % 64 == 0 && K % g == 0,
-               "%s: group_size=%d must be a multiple of 64 dividing K=%d", who, g, K);
+  // The decode kernels take any multiple of 32 (one scale group per 32-k step
+  // or more); the pipelined prefill kernel stages 64-k chunks of one group.
+  MM_CHECK_ARG(g > 0 && g % (M <= 32 ? 32 : 64) == 0 && K % g == 0,
+               "%s: group_size=%d must be a multiple of %d dividing K=%d", who, g,
+               M <= 32 ? 32 : 64, K);
   MM_CHECK_ARG(N % 8 == 0, "%s: N=%d must be divisible by 8", who, N);
   MM_CHECK_ARG(M > 32 || (size_t)N * (size_t)(K / 8) * 4 < ((size_t)1 << 32),
                "%s: each packed matrix must be under 4 GiB at M <= 32", who);

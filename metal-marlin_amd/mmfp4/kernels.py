@@ -128,7 +128,7 @@ def marlin_gemm_fp4(A: torch.Tensor, B_packed: torch.Tensor, scales: torch.Tenso
 
 def rowpacked_gemm_supported(M: int, N: int, K: int, group_size: int) -> bool:
     """Shapes mm_fp4_gemm_rowpacked takes (row-packed words read in place)."""
-    return (M > 0 and group_size > 0 and group_size % 64 == 0
+    return (M > 0 and group_size > 0 and group_size % (32 if M <= 32 else 64) == 0
             and K % group_size == 0 and N % (4 if M <= 32 else 8) == 0)
 
 
@@ -239,8 +239,8 @@ def mmfp4_fused_gate_up(x: torch.Tensor, gate_packed: torch.Tensor, gate_scales:
     """silu(gate_proj(x)) * up_proj(x) (kernels_core.py:4762-4774 ->
     MetalKernels.mmfp4_fused_gate_up :4269-4408).  Layout as documented there:
     gate_packed / up_packed row-packed [N, K/8] uint32, scales [K/group_size, N].
-    With group size % 64 == 0 and N % 8 == 0 the row-packed words are read
-    in place at every M (mm_fp4_gate_up_rowpacked: the decode
+    With N % 8 == 0 and a group size that is a multiple of 32 (up to 32 rows)
+    or of 64 (above) the row-packed words are read in place at every M (mm_fp4_gate_up_rowpacked: the decode
     kernel up to 32 rows, the pipelined prefill kernel above); other shapes
     are transposed to the Marlin layout on the device for each call (as the
     reference's own M < 64 path does); callers that keep the Marlin layout

@@ -3,11 +3,11 @@ mmfp4_linear.py:414-478, 549-598, 600-960).
 
 Row-packed means `packed_weights` uint32 [out_features, in_features // 8],
 word (n, j) holding inputs 8j..8j+7 of output n (LSB first); scales are
-[n_groups, out_features] or [out_features, n_groups].  When the group size
-is a multiple of 64 (and out_features % 8 == 0 above 32 rows), both the functional `mmfp4_gemm` and `MMFP4Linear` read the
-row-packed words in place at every M (mm_fp4_gemm_rowpacked: the decode
-kernels up to 32 rows, the pipelined prefill kernel above), so the layer
-holds one copy of its weights.  Other shapes run the Marlin-layout kernels
+[n_groups, out_features] or [out_features, n_groups].  Both the functional
+`mmfp4_gemm` and `MMFP4Linear` read the row-packed words in place
+(mm_fp4_gemm_rowpacked): the decode kernels up to 32 rows (group size a
+multiple of 32), the pipelined prefill kernel above (group size a multiple
+of 64, out_features % 8 == 0), so the layer holds one copy of its weights.  Other shapes run the Marlin-layout kernels
 on [in // 8, out] words: the functional form converts per call (as the
 reference does on every call); the layer converts once on the device and
 keeps the copy as a non-persistent buffer (the reference's

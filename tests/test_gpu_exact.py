@@ -117,7 +117,9 @@ def test_u4_gemm_bit_exact(rng, M, K, N, g, family):
                                      (512, 4096, 14336, 128), (48, 2880, 1024, 64),
                                      (100, 1408, 528, 64), (1, 2880, 1024, 64),
                                      (5, 896, 4864, 128), (13, 1408, 2048, 64),
-                                     (24, 2880, 516, 64), (32, 1408, 8192, 128)])
+                                     (24, 2880, 516, 64), (32, 1408, 8192, 128),
+                                     (1, 4096, 4096, 32), (9, 1440, 1024, 32),
+                                     (17, 2048, 520, 32), (32, 14336, 4096, 32)])
 def test_rowpacked_and_mmfp4_bit_exact(rng, M, K, N, g):
     """Row-packed words (both scale layouts) and Marlin words with [N, K/g]
     scales: the two-slab and skinny in-place variants (M <= 32, one and two

@@ -52,13 +52,14 @@ def test_gate_up_vs_fp32_reference(M, K, N, g):
                                      (16, 2048, 1024, 64), (40, 512, 256, 128),
                                      (300, 2048, 1000, 64), (64, 4096, 14336, 128),
                                      (40, 320, 256, 64), (1, 2880, 512, 64),
-                                     (24, 1408, 256, 64)])
+                                     (24, 1408, 256, 64), (1, 2048, 512, 32),
+                                     (20, 1440, 264, 32), (48, 1024, 256, 32)])
 def test_gate_up_rowpacked_vs_oracle(rng, M, K, N, g):
     """mmfp4_fused_gate_up on row-packed [N, K/8] weights (the reference's
     documented layout) against the numpy oracle: read in place by the decode
     kernel (M <= 16) and the pipelined prefill kernel (M > 16, including a
-    ragged N, a split-K grid and K % 256 != 0); group sizes that are not a
-    multiple of 64 are transposed per call."""
+    ragged N, a split-K grid and K % 256 != 0); g=32 is read in place up to
+    32 rows and transposed per call above."""
     import mmfp4
     wg = rng.normal(0, 0.02, (N, K)).astype(np.float16)
     wu = rng.normal(0, 0.02, (N, K)).astype(np.float16)

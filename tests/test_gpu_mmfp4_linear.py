@@ -108,9 +108,12 @@ def test_rowpacked_gemm_refuses_unsupported_shapes():
     s = torch.ones((64, 4), dtype=torch.float16, device="cuda")
     with pytest.raises(ValueError):                          # M > 32 needs N % 8 == 0
         mmfp4.mmfp4_gemm_rowpacked(a, rows[:60], s[:60], 128)
-    with pytest.raises(ValueError):                          # group size % 64 != 0
-        mmfp4.mmfp4_gemm_rowpacked(a[:1], rows, torch.ones((64, 16), dtype=torch.float16,
-                                                            device="cuda"), 32)
+    with pytest.raises(ValueError):                          # M > 32 needs g % 64 == 0
+        mmfp4.mmfp4_gemm_rowpacked(a, rows, torch.ones((16, 64), dtype=torch.float16,
+                                                       device="cuda"), 32)
+    with pytest.raises(ValueError):                          # g % 32 != 0
+        mmfp4.mmfp4_gemm_rowpacked(a[:1], rows, torch.ones((32, 64), dtype=torch.float16,
+                                                           device="cuda"), 16)
 
 
 @pytest.mark.parametrize("M,K,N,g", [(1, 4096, 4096, 128), (8, 14336, 4096, 128),
@@ -166,8 +169,9 @@ def test_mmfp4_gemm_rejects_mismatched_scales():
 def test_mmfp4_linear_reloaded_weights_take_effect(rng, g):
     """load_state_dict with new weights changes MMFP4Linear's output at every
     M and matches the oracle of the new weights: g=128 reads the row-packed
-    words in place at both sizes; g=32 (not a multiple of 64) runs the
-    Marlin-layout copy, which must follow writes to packed_weights."""
+    words in place at both sizes; g=32 in place at M=1 and, at M=40 (the
+    prefill kernel needs a multiple of 64), through the Marlin-layout copy,
+    which must follow writes to packed_weights."""
     import mmfp4
     out_f, in_f = 256, 512
     w1 = rng.normal(0, 0.02, (out_f, in_f)).astype(np.float16)
