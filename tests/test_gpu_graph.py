@@ -6,9 +6,9 @@ zero by the last block of each tile (no memset node).  So a caller can
 capture them: the four Llama-layer GEMMs (two-slab, skinny and split-K
 hand-off at M=1; the pipelined prefill kernel with and without its K split
 at M=128) and the MoE MLP (sort, grouped GEMMs, combine; decode- and
-prefill-sized groups) are captured once and replayed several times, with new
-inputs copied into the captured buffers and eager launches of the same
-entry points in between.  Every replay must equal the eager result on the
+prefill-sized groups), and the row-packed GEMM and gate/up pair, are
+captured once and replayed several times, with new inputs copied into the
+captured buffers and eager launches of the same entry points in between.  Every replay must equal the eager result on the
 same inputs bit for bit (the kernels are deterministic)."""
 
 from __future__ import annotations
@@ -109,3 +109,49 @@ def test_moe_mlp_graph_replay(T, E, k):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), rep
+
+
+@pytest.mark.parametrize("M", [1, 24, 64])
+def test_rowpacked_graph_replay(M):
+    """Row-packed (MMFP4) words read in place: the GEMM (split-K at M=1 on
+    14336 -> 4096, the two-row-block kernel at M=24, the pipelined kernel at
+    M=64, both scale layouts) and the gate/up pair with its SwiGLU."""
+    import mmfp4
+    gen = torch.Generator(device="cuda").manual_seed(101 + M)
+    shapes = [(14336, 4096), (4096, 6144)]
+    rows, scl = [], []
+    for K, N in shapes:
+        rows.append(torch.randint(-2**31, 2**31 - 1, (N, K // 8), generator=gen,
+                                  dtype=torch.int32, device="cuda"))
+        scl.append((torch.rand((K // G, N), generator=gen, device="cuda") * 0.01 + 1e-3).half())
+    gup = [torch.randint(-2**31, 2**31 - 1, (1536, 4096 // 8), generator=gen, dtype=torch.int32,
+                         device="cuda") for _ in range(2)]
+    gus = [(torch.rand((4096 // G, 1536), generator=gen, device="cuda") * 0.01 + 1e-3).half()
+           for _ in range(2)]
+    xs = {K: torch.empty((M, K), dtype=torch.float16, device="cuda") for K in (14336, 4096)}
+    scl_t = [s.t().contiguous() for s in scl]
+
+    def step():
+        outs = [mmfp4.mmfp4_gemm_rowpacked(xs[K], r, s, G)
+                for (K, _), r, s in zip(shapes, rows, scl)]
+        if M <= 32:
+            outs += [mmfp4.mmfp4_gemm_rowpacked(xs[K], r, s, G)
+                     for (K, _), r, s in zip(shapes, rows, scl_t)]
+        outs.append(mmfp4.mmfp4_fused_gate_up(xs[4096], gup[0], gus[0], gup[1], gus[1], G))
+        return outs
+
+    for x in xs.values():
+        x.copy_(torch.randn(x.shape, generator=gen, device="cuda").half())
+    announce(f"graph capture of the row-packed GEMMs M={M}")
+    g, outs = _capture(step)
+    for rep in range(4):
+        for x in xs.values():
+            x.copy_(torch.randn(x.shape, generator=gen, device="cuda").half())
+        torch.cuda.synchronize()
+        ref = step()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for i, (o, r) in enumerate(zip(outs, ref)):
+            assert torch.equal(o.view(torch.int16), r.view(torch.int16)), (rep, i)
+        mmfp4.mmfp4_gemm_rowpacked(xs[4096][:1], rows[1], scl[1], G)
