@@ -225,9 +225,11 @@ def _grouped(x, sorted_idx, offsets, gather: bool, k: int, T: int, packed, scale
         raise ValueError(f"activations K={x.shape[-1]} != packed K={K}")
     alloc = torch.zeros if zero_rows else torch.empty
     out = alloc((T * k, N // 2 if act else N), dtype=torch.float16, device=x.device)
+    # converted copies are bound to names so they outlive the launch
+    w, s = packed.contiguous(), scales.contiguous()
     _lib.call("mm_moe_grouped_gemm", _lib.ptr(x), _lib.ptr(sorted_idx), _lib.ptr(offsets),
-              int(gather), k, T, _lib.ptr(packed.contiguous()), _lib.ptr(scales.contiguous()),
-              E, K, N, group_size, act, _lib.ptr(out), _lib.stream_of(x))
+              int(gather), k, T, _lib.ptr(w), _lib.ptr(s), E, K, N, group_size, act,
+              _lib.ptr(out), _lib.stream_of(x))
     return out
 
 
@@ -291,9 +293,11 @@ def moe_mlp_fp4(hidden: torch.Tensor, gate_up_packed: torch.Tensor, gate_up_scal
     y = torch.empty((T * k, H), dtype=torch.float16, device=dev)
     sort_buf = torch.empty(E + 1 + 2 * T * k, dtype=torch.int32, device=dev)
     out = torch.empty((T, H), dtype=torch.float16, device=dev)
+    # converted copies are bound to names so they outlive the launch
+    gu, gus = gate_up_packed.contiguous(), _half(gate_up_scales)
+    dn, dns = down_packed.contiguous(), _half(down_scales)
     _lib.call("mm_moe_mlp_fp4", _lib.ptr(x), _lib.ptr(ids), int(i64), _lib.ptr(p), T, k, E, H, I,
-              _lib.ptr(gate_up_packed.contiguous()), _lib.ptr(_half(gate_up_scales)),
-              _lib.ptr(down_packed.contiguous()), _lib.ptr(_half(down_scales)), group_size,
+              _lib.ptr(gu), _lib.ptr(gus), _lib.ptr(dn), _lib.ptr(dns), group_size,
               _lib.ptr(act), _lib.ptr(y), _lib.ptr(sort_buf), _lib.ptr(out), _lib.stream_of(x))
     return out if hidden.dtype == torch.float16 else out.to(hidden.dtype)
 
@@ -403,9 +407,10 @@ def _moe_mlp_shared(hidden: torch.Tensor, routed, shared, expert_ids, expert_pro
     y = torch.empty((T * kt, H), dtype=torch.float16, device=dev)
     sort_buf = torch.empty(E + 2 + 2 * T * kt, dtype=torch.int32, device=dev)
     out = torch.empty((T, H), dtype=torch.float16, device=dev)
+    sgus_h, sdns_h = _half(sgus), _half(sdns)   # bound: they must outlive the launch
     _lib.call("mm_moe_mlp_shared_fp4", _lib.ptr(x), _lib.ptr(ids), i64, _lib.ptr(p), T, k, E, H,
               I, _lib.ptr(gu), _lib.ptr(gus), _lib.ptr(dn), _lib.ptr(dns), _lib.ptr(sgu),
-              _lib.ptr(_half(sgus)), _lib.ptr(sdn), _lib.ptr(_half(sdns)), float(shared_weight),
+              _lib.ptr(sgus_h), _lib.ptr(sdn), _lib.ptr(sdns_h), float(shared_weight),
               _lib.ptr(b), group_size, _lib.ptr(act), _lib.ptr(y), _lib.ptr(sort_buf),
               _lib.ptr(out), _lib.stream_of(x))
     return out

@@ -268,3 +268,65 @@ def test_moe_mlp_back_to_back_calls(rng):
             y, dp, md.MoEDispatchInfo(s_idx, s_idx, offs, inv, T, k, E, s_idx)))
     for o, r in zip(outs, refs):
         assert torch.equal(o, r)
+
+
+def test_moe_mlp_all_dropped_tokens_and_scale_dtypes(rng):
+    """Decode-sized groups: tokens whose every id is outside [0, E) come out
+    as exact zero rows, the others match the oracle with their dropped slots
+    contributing nothing; fp32 and bf16 scales (converted copies inside the
+    call, which must outlive the launches) give the same bits as fp16
+    scales."""
+    import mmfp4
+    E, T, k, H, I, g = 16, 24, 4, 512, 256, 128
+    GU, GS = _experts(rng, E, H, 2 * I, g)
+    DP, DS = _experts(rng, E, I, H, g)
+    x = rng.normal(0, 1, (T, H)).astype(np.float16)
+    ids, probs = omoe.router_topk(rng.normal(0, 1, (T, E)).astype(np.float32), k)
+    ids = ids.astype(np.int64)
+    bad = np.zeros((T, k), bool)
+    bad[[3, 7, 20]] = True                       # every slot of three tokens
+    bad[5, 1] = bad[11, 0] = bad[11, 3] = True   # some slots of others
+    ids[bad] = rng.choice([-1, E, E + 3], size=int(bad.sum()))
+    safe = np.where(bad, 0, ids).astype(np.int32)
+    ref = omoe.moe_forward_ref(x, GU, GS, DP, DS, safe, np.where(bad, 0.0, probs).astype(np.float32), g)
+    announce("moe mlp all-dropped tokens")
+    dx, dGU, dDP, dids, dp = to_dev(x), to_dev(GU), to_dev(DP), to_dev(ids), to_dev(probs)
+    out = mmfp4.moe_mlp_fp4(dx, dGU, to_dev(GS), dDP, to_dev(DS), dids, dp, g)
+    o = to_np(out)
+    assert np.array_equal(o[[3, 7, 20]], np.zeros((3, H), np.float16))
+    assert max_abs_rel(o, ref) <= TOL
+    for dt in (torch.float32, torch.bfloat16):
+        gs32, ds32 = to_dev(GS).to(dt), to_dev(DS).to(dt)
+        if dt == torch.bfloat16:                 # bf16 rounds the scales: compare with those
+            gs16, ds16 = gs32.half(), ds32.half()
+            want = mmfp4.moe_mlp_fp4(dx, dGU, gs16, dDP, ds16, dids, dp, g)
+        else:
+            want = out
+        got = mmfp4.moe_mlp_fp4(dx, dGU, gs32, dDP, ds32, dids, dp, g)
+        assert torch.equal(got, want), dt
+
+
+@pytest.mark.parametrize("T", [32, 1024])
+def test_moe_mlp_out_aliases_hidden(rng, T):
+    """mm_moe_mlp_fp4 with out == hidden (in place through the C ABI): the
+    combine, the only launch that writes out, runs after every read of the
+    hidden states, so the result matches the out-of-place call."""
+    import mmfp4
+    from mmfp4 import _lib
+    E, k, H, I, g = 32, 8, 512, 256, 128
+    GU, GS = _experts(rng, E, H, 2 * I, g)
+    DP, DS = _experts(rng, E, I, H, g)
+    ids, probs = omoe.router_topk(rng.normal(0, 1, (T, E)).astype(np.float32), k)
+    x = to_dev(rng.normal(0, 1, (T, H)).astype(np.float16))
+    dGU, dGS, dDP, dDS = to_dev(GU), to_dev(GS), to_dev(DP), to_dev(DS)
+    dids, dp = to_dev(ids.astype(np.int32)), to_dev(probs)
+    announce(f"moe mlp in place T={T}")
+    want = mmfp4.moe_mlp_fp4(x, dGU, dGS, dDP, dDS, dids, dp, g)
+    xin = x.clone()
+    act = torch.empty((T * k, I), dtype=torch.float16, device="cuda")
+    y = torch.empty((T * k, H), dtype=torch.float16, device="cuda")
+    sort_buf = torch.empty(E + 1 + 2 * T * k, dtype=torch.int32, device="cuda")
+    _lib.call("mm_moe_mlp_fp4", _lib.ptr(xin), _lib.ptr(dids), 0, _lib.ptr(dp), T, k, E, H, I,
+              _lib.ptr(dGU), _lib.ptr(dGS), _lib.ptr(dDP), _lib.ptr(dDS), g, _lib.ptr(act),
+              _lib.ptr(y), _lib.ptr(sort_buf), _lib.ptr(xin), _lib.stream_of(xin))
+    assert torch.equal(xin, want)
