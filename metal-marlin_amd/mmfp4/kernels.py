@@ -211,6 +211,15 @@ def _gate_up(x: torch.Tensor, gate_packed: torch.Tensor, gate_scales: torch.Tens
                          f"K={K_packed * FP4_PER_UINT}")
     _check_groups("gate_scales", gate_scales, K, N, group_size)
     _check_groups("up_scales", up_scales, K, N, group_size)
+    if M > 32 and K % 64 != 0 and N % 8 == 0:
+        # The one-launch pair kernel above 32 rows streams 64-k chunks; other
+        # K take two GEMM launches (the tile kernel for K % 64 tails), and
+        # SiLU then sees the fp16 products, as in the reference's kernel.
+        g = marlin_gemm_fp4(x, gate_packed, gate_scales, group_size)
+        u = marlin_gemm_fp4(x, up_packed, up_scales, group_size)
+        if not act:
+            return torch.cat([g, u], dim=1)
+        return (torch.nn.functional.silu(g.float()) * u.float()).half()
     a = _half(x)
     out = torch.empty((M, N if act else 2 * N), dtype=torch.float16, device=dev)
     ws_bytes = int(_lib.load().mm_gemm_workspace_bytes(M, 2 * N, K))
@@ -240,8 +249,9 @@ def mmfp4_fused_gate_up(x: torch.Tensor, gate_packed: torch.Tensor, gate_scales:
     MetalKernels.mmfp4_fused_gate_up :4269-4408).  Layout as documented there:
     gate_packed / up_packed row-packed [N, K/8] uint32, scales [K/group_size, N].
     With N % 8 == 0 and a group size that is a multiple of 32 (up to 32 rows)
-    or of 64 (above) the row-packed words are read in place at every M (mm_fp4_gate_up_rowpacked: the decode
-    kernel up to 32 rows, the pipelined prefill kernel above); other shapes
+    or of 64 (above) the row-packed words are read in place at every M
+    (mm_fp4_gate_up_rowpacked: the decode kernel up to 32 rows, the
+    pipelined prefill kernel above); other shapes
     are transposed to the Marlin layout on the device for each call (as the
     reference's own M < 64 path does); callers that keep the Marlin layout
     call `mmfp4_fused_gate_up_marlin`.

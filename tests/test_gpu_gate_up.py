@@ -27,7 +27,8 @@ def _weights(gen, K, N, g):
                                      (16, 14336, 512, 128), (17, 2048, 1024, 32),
                                      (32, 4096, 2048, 128), (33, 1024, 512, 128),
                                      (64, 4096, 1024, 64), (200, 2048, 1544, 128),
-                                     (512, 4096, 4096, 128), (130, 256, 136, 32)])
+                                     (512, 4096, 4096, 128), (130, 256, 136, 32),
+                                     (48, 200, 128, 8), (40, 1000, 264, 8)])
 def test_gate_up_vs_fp32_reference(M, K, N, g):
     import mmfp4
     gen = torch.Generator(device="cuda").manual_seed(M * 7 + N)
