@@ -14,9 +14,9 @@ from pathlib import Path
 PKG = Path(__file__).resolve().parents[1] / "metal-marlin_amd" / "mmfp4"
 
 
-def _offenders():
+def _offenders(root: Path = PKG):
     out = []
-    for f in sorted(PKG.rglob("*.py")):
+    for f in sorted(root.rglob("*.py")):
         tree = ast.parse(f.read_text(), filename=str(f))
         for node in ast.walk(tree):
             if not isinstance(node, ast.Call):
@@ -24,7 +24,7 @@ def _offenders():
             fn = node.func
             name = fn.attr if isinstance(fn, ast.Attribute) else getattr(fn, "id", "")
             if name == "ptr" and node.args and isinstance(node.args[0], ast.Call):
-                out.append(f"{f.relative_to(PKG.parent)}:{node.lineno}: {ast.unparse(node)}")
+                out.append(f"{f.relative_to(root.parent)}:{node.lineno}: {ast.unparse(node)}")
     return out
 
 
@@ -33,9 +33,11 @@ def test_no_pointer_to_a_temporary():
 
 
 def test_guard_sees_the_pattern(tmp_path):
-    # the scan itself flags the pattern it guards against
-    src = "def f(_lib, s):\n    return _lib.ptr(s.contiguous())\n"
-    tree = ast.parse(src)
-    calls = [n for n in ast.walk(tree) if isinstance(n, ast.Call)
-             and getattr(n.func, "attr", "") == "ptr" and isinstance(n.args[0], ast.Call)]
-    assert len(calls) == 1
+    """The scan flags a pointer to a converted copy and passes a named one."""
+    pkg = tmp_path / "pkg"
+    pkg.mkdir()
+    (pkg / "bad.py").write_text("def f(_lib, s):\n    return _lib.ptr(s.contiguous())\n")
+    (pkg / "good.py").write_text("def f(_lib, s):\n    c = s.contiguous()\n"
+                                 "    return _lib.ptr(c)\n")
+    found = _offenders(pkg)
+    assert len(found) == 1 and "bad.py:2" in found[0]
