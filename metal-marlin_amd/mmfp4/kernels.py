@@ -52,6 +52,18 @@ def _ws_bytes(M: int, N: int, K: int) -> int:
 
 def _gemm(kind: str, A: torch.Tensor, B_packed: torch.Tensor, scales: torch.Tensor,
           zeros: torch.Tensor | None, group_size: int) -> torch.Tensor:
+    N = B_packed.shape[-1] if B_packed.dim() == 2 else 0
+    if N % 4 != 0 and scales.dim() == 2 and scales.shape[-1] == N and \
+            (zeros is None or (zeros.dim() == 2 and zeros.shape[-1] == N)):
+        # The kernels store 4 adjacent columns per lane.  Other widths (an
+        # lm_head over 32001 tokens, say) run on copies padded to a multiple
+        # of 4 -- zero words, unit scales, zero points 0, so the extra columns
+        # are exact zeros -- and return the first N columns.
+        pad = (0, -N % 4)
+        zp = None if zeros is None else torch.nn.functional.pad(zeros, pad)
+        out = _gemm(kind, A, torch.nn.functional.pad(B_packed, pad),
+                    torch.nn.functional.pad(scales, pad, value=1.0), zp, group_size)
+        return out[..., :N].contiguous()
     fast = _BINDING if _BINDING is not None else _binding()
     if fast:
         # checks, output allocation and workspace in C++ (_mmfp4_torch.so)

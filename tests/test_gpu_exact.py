@@ -202,3 +202,21 @@ def test_grouped_gemm_bit_exact(rng, T, k, E, K, N):
         if r1 > r0:
             ref[r0:r1] = ofp4.gemm_fp4_ref(x[s_np[r0:r1] // k], P[e], S[e], g)
     _same(y, ref)
+
+
+@pytest.mark.parametrize("M,N", [(1, 1002), (9, 2001), (40, 1001), (300, 523)])
+def test_odd_width_bit_exact(rng, M, N):
+    """marlin_gemm_fp4 / marlin_gemm_int4 with N % 4 != 0 (the kernels store
+    4 adjacent columns per lane): the operator pads a copy and returns the
+    first N columns, bit-exact against the oracle."""
+    import mmfp4
+    K, g = 512, 64
+    packed, scales = _exact_fp4(rng, K, N, g)
+    a = _acts(rng, M, K)
+    announce(f"exact odd width M={M} N={N}")
+    out = mmfp4.marlin_gemm_fp4(to_dev(a), to_dev(packed), to_dev(scales), g)
+    assert tuple(out.shape) == (M, N) and out.is_contiguous()
+    _same(out, ofp4.gemm_fp4_ref(a, packed, scales, g))
+    q, s, z = _exact_u4(rng, K, N, g)
+    _same(mmfp4.marlin_gemm_int4(to_dev(a), to_dev(q), to_dev(s), to_dev(z), g),
+          ofp4.gemm_u4_ref(a, q, s, z, g))
