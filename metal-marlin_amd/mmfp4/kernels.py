@@ -223,10 +223,11 @@ def _gate_up(x: torch.Tensor, gate_packed: torch.Tensor, gate_scales: torch.Tens
                          f"K={K_packed * FP4_PER_UINT}")
     _check_groups("gate_scales", gate_scales, K, N, group_size)
     _check_groups("up_scales", up_scales, K, N, group_size)
-    if M > 32 and K % 64 != 0 and N % 8 == 0:
-        # The one-launch pair kernel above 32 rows streams 64-k chunks; other
-        # K take two GEMM launches (the tile kernel for K % 64 tails), and
-        # SiLU then sees the fp16 products, as in the reference's kernel.
+    if N % 8 != 0 or (M > 32 and K % 64 != 0):
+        # The one-launch pair kernels take N % 8 == 0, and above 32 rows
+        # stream 64-k chunks; other shapes take two GEMM launches (any N, and
+        # the tile kernel for K % 64 tails), and SiLU then sees the fp16
+        # products, as in the reference's kernel.
         g = marlin_gemm_fp4(x, gate_packed, gate_scales, group_size)
         u = marlin_gemm_fp4(x, up_packed, up_scales, group_size)
         if not act:
