@@ -335,6 +335,12 @@ def mmfp4_fused_qkv(A: torch.Tensor, Q_packed: torch.Tensor, Q_scales: torch.Ten
         mats.append((_packed(p), _half(sc)))
     a = _half(A.reshape(M, Kdim))
     Ns = [p.shape[1] for p, _ in mats]
+    lead = tuple(orig_shape[:-1]) if len(orig_shape) > 1 else (1,)
+    if any(n % 4 for n in Ns):
+        # the one-launch form stores 4 adjacent columns per lane; other widths
+        # take one (padded) GEMM per matrix
+        return tuple(marlin_gemm_fp4(a, p, sc, group_size).reshape(*lead, n)
+                     for (p, sc), n in zip(mats, Ns))
     outs = [torch.empty((M, n), dtype=torch.float16, device=dev) for n in Ns]
     lib = _lib.load()
     ws_bytes = max([int(lib.mm_gemm_workspace_bytes(M, sum(Ns), Kdim))] +
@@ -347,7 +353,6 @@ def mmfp4_fused_qkv(A: torch.Tensor, Q_packed: torch.Tensor, Q_scales: torch.Ten
     Nt = (ctypes.c_int * 3)(*Ns)
     _lib.call("mm_fp4_gemm_multi", _lib.ptr(a), 3, Bt, St, Ct, Nt, M, Kdim, group_size,
               _lib.ptr(ws), ws.numel(), _lib.stream_of(a))
-    lead = tuple(orig_shape[:-1]) if len(orig_shape) > 1 else (1,)
     return tuple(o.reshape(*lead, n) for o, n in zip(outs, Ns))
 
 

@@ -26,7 +26,8 @@ def _weights(gen, K, N, g):
                                       (16, 14336, (512, 256, 256), 128),
                                       (17, 4096, (4096, 1024, 1024), 128),
                                       (64, 4096, (4096, 1024, 1024), 128),
-                                      (3, 1024, (260, 132, 68), 32)])
+                                      (3, 1024, (260, 132, 68), 32),
+                                      (1, 512, (258, 130, 64), 64)])
 def test_fused_qkv_vs_fp32_reference(M, K, Ns, g):
     import mmfp4
     gen = torch.Generator(device="cuda").manual_seed(M + K)
