@@ -61,7 +61,8 @@ def _gemm(kind: str, A: torch.Tensor, B_packed: torch.Tensor, scales: torch.Tens
         # are exact zeros -- and return the first N columns.
         pad = (0, -N % 4)
         zp = None if zeros is None else torch.nn.functional.pad(zeros, pad)
-        out = _gemm(kind, A, torch.nn.functional.pad(B_packed, pad),
+        words = B_packed.view(torch.int32) if B_packed.dtype == torch.uint32 else B_packed
+        out = _gemm(kind, A, torch.nn.functional.pad(words, pad),
                     torch.nn.functional.pad(scales, pad, value=1.0), zp, group_size)
         return out[..., :N].contiguous()
     fast = _BINDING if _BINDING is not None else _binding()

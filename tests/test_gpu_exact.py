@@ -217,6 +217,9 @@ def test_odd_width_bit_exact(rng, M, N):
     out = mmfp4.marlin_gemm_fp4(to_dev(a), to_dev(packed), to_dev(scales), g)
     assert tuple(out.shape) == (M, N) and out.is_contiguous()
     _same(out, ofp4.gemm_fp4_ref(a, packed, scales, g))
+    words_u32 = to_dev(packed).view(torch.uint32)         # uint32 words take the same path
+    _same(mmfp4.marlin_gemm_fp4(to_dev(a), words_u32, to_dev(scales), g),
+          ofp4.gemm_fp4_ref(a, packed, scales, g))
     q, s, z = _exact_u4(rng, K, N, g)
     _same(mmfp4.marlin_gemm_int4(to_dev(a), to_dev(q), to_dev(s), to_dev(z), g),
           ofp4.gemm_u4_ref(a, q, s, z, g))
