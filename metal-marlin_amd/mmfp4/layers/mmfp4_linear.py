@@ -112,18 +112,27 @@ class MMFP4Linear(nn.Module):
         self.out_features = out_f
         self.activation = activation
 
-    def _kernel_weights(self, device: torch.device) -> torch.Tensor:
-        # The Marlin-layout copy is keyed on the source buffer's identity and
-        # version counter, so load_state_dict / copy_ into packed_weights (or a
-        # new tensor assigned to it) rebuilds it.
-        src = self.packed_weights
-        key = (src.data_ptr(), src._version, device)
+    def _kernel_weights(self, device: torch.device):
+        """(Marlin-layout words, scales or None).  The copy is keyed on the
+        source buffers' identity and version counters, so load_state_dict /
+        copy_ into packed_weights or scales (or new tensors assigned to them)
+        rebuilds it.  With out_features % 4 != 0 the words and scales are
+        padded to a multiple of 4 columns here, once, instead of per call."""
+        src, sc = self.packed_weights, self.scales
+        pad = -self.out_features % 4
+        key = (src.data_ptr(), src._version, device) + \
+            ((sc.data_ptr(), sc._version) if pad else ())
         kp = self._kernel_packed_weights
         if kp is None or getattr(self, "_kernel_key", None) != key:
             kp = rowpacked_to_marlin(src.to(device))
+            self._kernel_scales = None
+            if pad:
+                kp = torch.nn.functional.pad(kp.view(torch.int32), (0, pad))
+                self._kernel_scales = torch.nn.functional.pad(
+                    sc.to(device=device, dtype=torch.float16), (0, pad), value=1.0)
             self._kernel_packed_weights = kp
             self._kernel_key = key
-        return kp
+        return kp, self._kernel_scales
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if x.shape[-1] != self.in_features:
@@ -138,8 +147,9 @@ class MMFP4Linear(nn.Module):
             out = kernels.mmfp4_gemm_rowpacked(x2, self.packed_weights.to(x.device), scales,
                                                self.group_size)
         else:
-            out = kernels.marlin_gemm_fp4(x2, self._kernel_weights(x.device), scales,
-                                          self.group_size)
+            kp, ks = self._kernel_weights(x.device)
+            out = kernels.marlin_gemm_fp4(x2, kp, scales if ks is None else ks, self.group_size)
+            out = out[:, :self.out_features] if ks is not None else out
         if self.bias is not None:
             out = out + self.bias.to(device=out.device, dtype=out.dtype)
         out = out.reshape(*x.shape[:-1], self.out_features)

@@ -192,3 +192,28 @@ def test_mmfp4_linear_reloaded_weights_take_effect(rng, g):
         assert max_abs_rel(to_np(y2), ofp4.gemm_fp4_ref(x, m2, s2, g)) <= TOL
         layer.load_state_dict({"packed_weights": to_dev(np.ascontiguousarray(m1.T).view(np.int32)),
                                "scales": to_dev(s1)}, strict=False)
+
+
+def test_mmfp4_linear_odd_width(rng):
+    """out_features % 4 != 0: the layer pads its Marlin-layout copy (and its
+    scales) to a multiple of 4 columns once, reuses it across calls, rebuilds
+    it when the scales are written, and returns out_features columns that
+    match the oracle."""
+    import mmfp4
+    out_f, in_f, g = 1002, 512, 64
+    w = rng.normal(0, 0.02, (out_f, in_f)).astype(np.float16)
+    m, s = ofp4.quantize_fp4(w, g)
+    layer = mmfp4.MMFP4Linear(to_dev(np.ascontiguousarray(m.T).view(np.int32)), to_dev(s), None, g)
+    for M in (1, 40):
+        x = rng.normal(0, 1, (M, in_f)).astype(np.float16)
+        announce(f"MMFP4Linear odd width M={M}")
+        y = layer(to_dev(x))
+        assert tuple(y.shape) == (M, out_f)
+        assert max_abs_rel(to_np(y), ofp4.gemm_fp4_ref(x, m, s, g)) <= TOL
+    kp = layer._kernel_packed_weights
+    layer(to_dev(x))
+    assert layer._kernel_packed_weights is kp            # reused, not re-padded
+    s2 = (s * 2).astype(np.float16)
+    layer.load_state_dict({"scales": to_dev(s2)}, strict=False)
+    y2 = layer(to_dev(x))
+    assert max_abs_rel(to_np(y2), ofp4.gemm_fp4_ref(x, m, s2, g)) <= TOL
