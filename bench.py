@@ -135,7 +135,7 @@ def run_read_ceiling(torch, steps: int, warmup: int):
     decode, no math) over each layer GEMM's packed weights + scales, rotated
     copies, timed exactly like the GEMMs.  The practical ceiling of a
     weight-streaming kernel of that size (launch, ramp-up and drain included)."""
-    from mmfp4 import _lib
+    import bench_aids
     sizes = [(name, -(-alg_bytes(0, K, N) // 16) * 16) for name, K, N in LLAMA_LAYER]
     copies = max(2, -(-ROTATE_BYTES // sum(b for _, b in sizes)))
     bufs = [[torch.empty(b, dtype=torch.uint8, device="cuda") for _, b in sizes]
@@ -144,8 +144,8 @@ def run_read_ceiling(torch, steps: int, warmup: int):
     st = torch.cuda.current_stream().cuda_stream
 
     def rd(buf):
-        return lambda: _lib.call("mm_stream_read", buf.data_ptr(), buf.numel(), sink.data_ptr(),
-                                 sink.numel() * 4, st)
+        return lambda: bench_aids.call("mm_stream_read", buf.data_ptr(), buf.numel(),
+                                       sink.data_ptr(), sink.numel() * 4, 0, 0, 4, 1, st)
     launches = [[rd(b) for b in row] for row in bufs]
     total_ms = timed_launches(torch, launches, steps, warmup)
     per = {name: round(us, 3) for (name, _), us in zip(sizes, per_shape_us(torch, launches))}
@@ -186,7 +186,7 @@ def run_mfma_ceiling(torch, mmfp4, prefill_tflops: float):
     config-4 matrices -- and (b) all-ones operands.  The board's power limit
     lowers the clock as more operand bits toggle, so (a) is the practical
     matrix-core ceiling of this GEMM and (b) shows the dense peak."""
-    from mmfp4 import _lib
+    import bench_aids
     n = 1 << 20
     gen = torch.Generator(device="cuda").manual_seed(11)
     acts = torch.randn(n, generator=gen, device="cuda").half()
@@ -200,8 +200,9 @@ def run_mfma_ceiling(torch, mmfp4, prefill_tflops: float):
     res = {"kernel": "mm_mfma_ceiling (MFMA 32x32x16 f16 only, 256 blocks x 8 waves)"}
     for name, a, b in (("gemm_operands", acts, wdq), ("ones", ones, ones)):
         nh = min(a.numel(), b.numel()) // 8 * 8
-        fn = lambda a=a, b=b, nh=nh: _lib.call("mm_mfma_ceiling", a.data_ptr(), b.data_ptr(), nh,
-                                               iters, sink.data_ptr(), sink.numel() * 4, st)
+        fn = lambda a=a, b=b, nh=nh: bench_aids.call("mm_mfma_ceiling", a.data_ptr(), b.data_ptr(),
+                                                     nh, iters, sink.data_ptr(), sink.numel() * 4,
+                                                     st)
         ms = timed_launches(torch, [[fn]], 40, 40)
         res[name + "_tflops"] = round(flops * 40 / (ms * 1e-3) / 1e12, 1)
     res["prefill_fraction_of_gemm_operand_ceiling"] = round(

@@ -298,26 +298,6 @@ int mm_fp4_flat_dequantize(const uint8_t* codes, const float* scales, size_t n, 
  * metal_marlin/fp4_metal.py:278-300 (FP4Metal.pack_pair). */
 int mm_fp4_pack_pair(const uint8_t* lo, const uint8_t* hi, size_t n, uint8_t* out, void* stream);
 
-/* ------------------------------------------------------------ measurement */
-
-/* Reads `bytes` (a multiple of 16, 16-byte aligned) of device memory once
- * and writes nothing (sink: a scratch buffer of at least 4 MiB that a sentinel
- * test keeps the loads alive for).  No counterpart in the reference: a
- * measurement aid that gives the HBM read rate reachable for that many bytes
- * in back-to-back launches, the practical ceiling of a weight-streaming GEMM
- * of the same size. */
-int mm_stream_read(const void* p, size_t bytes, uint32_t* sink, size_t sink_bytes, void* stream);
-
-/* Runs MFMA 32x32x16 f16 and nothing else on 256 blocks of 8 waves (one block
- * per CU), with operand values taken from a and b (n_halves fp16 each, a
- * multiple of 8, 16-byte aligned); sink receives 256 x 512 floats.  One launch
- * performs 256 * 8 * iters * 32 MFMAs of 32768 flops.  No counterpart in the
- * reference: a measurement aid for the sustained matrix-core rate with a
- * GEMM's own operand values (the rate falls as more operand bits toggle,
- * because the board's power limit lowers the clock). */
-int mm_mfma_ceiling(const uint16_t* a, const uint16_t* b, size_t n_halves, int iters, float* sink,
-                    size_t sink_bytes, void* stream);
-
 #ifdef __cplusplus
 }
 #endif

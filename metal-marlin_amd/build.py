@@ -1,6 +1,8 @@
 """Build libmmfp4.so (gfx950) in-tree: every csrc/*.hip -> object -> one shared
 library next to the Python package (mmfp4/libmmfp4.so), plus the per-call torch
-binding mmfp4/_mmfp4_torch.so (csrc/mm_pybind.cpp, host C++ linked to it).
+binding mmfp4/_mmfp4_torch.so (csrc/mm_pybind.cpp, host C++ linked to it) and
+bench.py's measurement aids bench_aids/libmmfp4_bench.so (not part of the
+GEMM library's ABI).
 
 Usage: python metal-marlin_amd/build.py [-j N]
 """
@@ -21,6 +23,9 @@ BUILD = HERE / "_build"
 LIB = HERE / "mmfp4" / "libmmfp4.so"
 BIND_SRC = CSRC / "mm_pybind.cpp"
 BIND = HERE / "mmfp4" / "_mmfp4_torch.so"
+# Measurement aids for bench.py, kept out of the GEMM library's ABI.
+AIDS_SRC = HERE / "bench_aids" / "mm_bench_aids.hip"
+AIDS = HERE / "bench_aids" / "libmmfp4_bench.so"
 ROOT = HERE.parent
 
 ARCH = "gfx950"
@@ -61,8 +66,10 @@ def build(jobs: int | None = None) -> Path:
     jobs = jobs or min(len(srcs), os.cpu_count() or 4, 16)
     with cf.ThreadPoolExecutor(jobs + 1) as ex:
         bind_obj = ex.submit(compile_binding)
+        aids_obj = ex.submit(_compile, cc, AIDS_SRC)
         objs = list(ex.map(lambda s: _compile(cc, s), srcs))
         bind_obj = bind_obj.result()
+        aids_obj = aids_obj.result()
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -70,6 +77,12 @@ def build(jobs: int | None = None) -> Path:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{r.stderr}")
     os.replace(tmp, LIB)
     link_binding(bind_obj)
+    cmd = [cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-Bsymbolic", "-o",
+           str(AIDS.with_suffix(".so.tmp")), str(aids_obj)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link failed: {' '.join(cmd)}\n{r.stderr}")
+    os.replace(AIDS.with_suffix(".so.tmp"), AIDS)
     return LIB
 
 

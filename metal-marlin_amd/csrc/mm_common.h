@@ -105,3 +105,23 @@ void mm_set_error(const char* fmt, ...);
   } while (0)
 
 __host__ __device__ static inline int mm_cdiv(int a, int b) { return (a + b - 1) / b; }
+
+// ---------------------------------------------------------------------------
+// 16-byte accesses coherent across the XCDs' L2s (the cache policy the
+// compiler gives agent-scope atomic loads and stores on gfx950: sc1), for the
+// split-K partial sums: a raw buffer resource over the partial-sum array, so a
+// lane moves 4 floats per instruction instead of 4 scalar atomics.
+// ---------------------------------------------------------------------------
+MM_DEV __amdgpu_buffer_rsrc_t mm_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff,
+                                           0x00020000);
+}
+constexpr int MM_CPOL_SC1 = 16;
+MM_DEV f32x4 load_agent_x4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0,
+                                                                         MM_CPOL_SC1));
+}
+MM_DEV void store_agent_x4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, f32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, byte_off, 0,
+                                         MM_CPOL_SC1);
+}

@@ -189,10 +189,12 @@ k_skinny(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
     return;
   }
   // K split across blocks: publish this block's partial tile, then the last
-  // block of the column tile sums all partials in split order.  Partials and
-  // the counter are accessed with agent-scope atomics (coherent across the
-  // XCDs' L2s without writing back whole caches); a workgroup-scope release
-  // (wait for this wave's stores) orders the stores before the counter bump.
+  // block of the column tile sums all partials in split order.  Partials are
+  // moved with 16-byte sc1 buffer accesses (the agent-scope policy: coherent
+  // across the XCDs' L2s without writing back whole caches) and the counter
+  // with an agent-scope atomic; waiting for this wave's stores orders them
+  // before the counter bump.
+  const __amdgpu_buffer_rsrc_t prs = mm_rsrc(part);
   if (wave == 0) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
@@ -202,20 +204,17 @@ k_skinny(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
           const int row = mt * 16 + 4 * q + rr;
-          if (row < M && col < N) {
-            float* dst = part + ((size_t)blockIdx.y * M + row) * PW + pcol(t);
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-              __hip_atomic_store(dst + j, acc[mt][t][j][rr], __ATOMIC_RELAXED,
-                                 __HIP_MEMORY_SCOPE_AGENT);
-          }
+          if (row < M && col < N)
+            store_agent_x4(prs, 4u * (uint32_t)((blockIdx.y * M + row) * PW + pcol(t)),
+                           f32x4{acc[mt][t][0][rr], acc[mt][t][1][rr], acc[mt][t][2][rr],
+                                 acc[mt][t][3][rr]});
         }
       }
   }
-  // Hand-off.  The partials are agent-scope atomic stores (coherent across
-  // the XCDs' L2s); s_waitcnt(0) waits until they are performed at that
-  // coherence point before thread 0 (of the same wave 0) bumps the arrival
-  // counter, and the last block reads them with agent-scope atomic loads.
+  // Hand-off.  The partials are sc1 stores (coherent across the XCDs' L2s);
+  // s_waitcnt(0) waits until they are performed at that coherence point
+  // before thread 0 (of the same wave 0) bumps the arrival counter, and the
+  // last block reads them with sc1 loads.
   // This is the ordering the ISA gives a wave's memory operations.  The
   // language-level form (release increment, acquire read) was measured: the
   // agent-scope release writes back the whole L2 (buffer_wbl2) and took the
@@ -239,10 +238,7 @@ k_skinny(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
 #pragma unroll
       for (int i = 0; i < SK_RED_BATCH; ++i) {
         const int y = min(y0 + i, ksplit - 1);
-        const float* src = part + ((size_t)y * M + row) * PW + pc;
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          ld[i][j] = __hip_atomic_load(src + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        ld[i] = load_agent_x4(prs, 4u * (uint32_t)((y * M + row) * PW + pc));
       }
 #pragma unroll
       for (int i = 0; i < SK_RED_BATCH; ++i)
@@ -562,7 +558,7 @@ __global__ void __launch_bounds__(WM * WN * 64)
 k_prefill2(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
            const f16* __restrict__ S, const f16* __restrict__ Z, const uint32_t* __restrict__ B2,
            const f16* __restrict__ S2, const f16* __restrict__ Z2, f16* __restrict__ C, int ldc,
-           int M, int N, int K, int g, float* __restrict__ part) {
+           int M, int N, int K, int g, float* __restrict__ part, int grp) {
   // Wave tile: (32*RB) rows x (32*CW) LDS columns.  SK_PLAIN: lane l32 owns
   // CW adjacent columns (CW packed words of one word row feed CW column
   // tiles).  Pair modes (CW = 2, tile-major): column tile 0 is 32 gate
@@ -576,13 +572,28 @@ k_prefill2(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / WN, wn = wave % WN;
   const int l32 = lane & 31, h = lane >> 5;
-  const int m0 = blockIdx.y * Sh::BM;
-  const int n0 = blockIdx.x * (ACT == SK_PLAIN ? Sh::BN : Sh::BN / 2);
-  // K split: blockIdx.z owns chunks [c_beg, c_end); with gridDim.z > 1 the
+  // Tile placement.  Blocks are dealt round-robin to the 8 XCDs by linear id,
+  // so the linear id is first remapped to give XCD x one contiguous run of
+  // tile indices, and a tile index then walks groups of `grp` row tiles
+  // column by column.  One XCD's run is about grp row tiles x (run / grp)
+  // column tiles: an A row tile and a B column tile are each fetched by a
+  // few XCDs instead of by all eight (the grid's x and y only count tiles).
+  const int nx = gridDim.x, ny = gridDim.y;
+  const int ntile = nx * ny * gridDim.z;
+  const int L = blockIdx.x + nx * (blockIdx.y + ny * blockIdx.z);
+  const int xq = ntile >> 3, xr = ntile & 7, xcd = L & 7;
+  const int lin = xcd * xq + min(xcd, xr) + (L >> 3);
+  const int bz = lin / (nx * ny), lt = lin - bz * (nx * ny);
+  const int gi = lt / (grp * nx), gw = lt - gi * (grp * nx);
+  const int gr = min(grp, ny - gi * grp);
+  const int by = gi * grp + gw % gr, bx = gw / gr;
+  const int m0 = by * Sh::BM;
+  const int n0 = bx * (ACT == SK_PLAIN ? Sh::BN : Sh::BN / 2);
+  // K split: split bz owns chunks [c_beg, c_end); with gridDim.z > 1 the
   // tile is written as an fp32 partial to part[z][M][PW] instead of C.
   const int nch_all = K / PF2_BK;
   const int cps = (nch_all + gridDim.z - 1) / gridDim.z;
-  const int c_beg = blockIdx.z * cps;
+  const int c_beg = bz * cps;
   const int c_end = min(nch_all, c_beg + cps);
   f32x16 acc[RB][CW];
   if constexpr (ROWS && ACT == SK_PLAIN) {
@@ -624,10 +635,10 @@ k_prefill2(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
           fvec o;
 #pragma unroll
           for (int j = 0; j < CW; ++j) o[j] = acc[rb][j][v];
-          *(fvec*)(part + ((size_t)blockIdx.z * M + row) * PW + ncol) = o;
+          *(fvec*)(part + ((size_t)bz * M + row) * PW + ncol) = o;
         }
       } else if (gridDim.z > 1) {
-        float* prow = part + ((size_t)blockIdx.z * M + row) * PW;
+        float* prow = part + ((size_t)bz * M + row) * PW;
         prow[ncol] = acc[rb][0][v];
         prow[N + ncol] = acc[rb][1][v];
       } else if constexpr (ACT == SK_SWIGLU) {
@@ -932,19 +943,39 @@ size_t prefill_ws_bytes(int M, int N, int K) {
   return p.ksplit > 1 ? (size_t)p.ksplit * M * N * sizeof(float) : 0;
 }
 
+// Row-group height of k_prefill2's tile walk.  One XCD's run of tiles
+// covers about grp row tiles x (run / grp) column tiles; each of its row
+// tiles costs BM x 2 bytes of A per k and each column tile BN x 0.5 bytes of
+// B (+ INT4 zeros: BN x ~0.03), so pick the power of two that minimises the
+// XCD's A + B fetch.
+int prefill_row_group(int nx, int ny, int nz, int BM, int BN, bool int4) {
+  const int run = std::max(1, nx * ny * nz / 8);
+  const double bcost = BN * (int4 ? 0.53 : 0.5);
+  int best = 1;
+  double best_cost = 1e300;
+  for (int r = 1; r <= ny; r *= 2) {
+    const int rows = std::min(ny, std::max(r, (run + nx - 1) / nx));
+    const int cols = std::min(nx, (run + rows - 1) / rows);
+    const double cost = rows * BM * 2.0 + cols * bcost;
+    if (cost < best_cost) { best_cost = cost; best = r; }
+  }
+  return best;
+}
+
 template <bool INT4, int ACT, int WM, int WN, int RB, int CW, bool ROWS = false>
 int launch_prefill2(const f16* A, int lda, const uint32_t* B, const f16* S, const f16* Z,
                     const uint32_t* B2, const f16* S2, const f16* Z2, f16* C, int ldc, int M,
                     int N, int K, int g, int ks, float* part, hipStream_t st) {
   constexpr int BM = WM * 32 * RB, BN = WN * 32 * CW;
   dim3 grid(mm_cdiv(N, ACT == SK_PLAIN ? BN : BN / 2), mm_cdiv(M, BM), ks);
+  const int grp = prefill_row_group((int)grid.x, (int)grid.y, (int)grid.z, BM, BN, INT4);
   if (g % PF2_BK == 0)
     hipLaunchKernelGGL((k_prefill2<INT4, WM, WN, RB, CW, true, ACT, ROWS>), grid,
                        dim3(WM * WN * 64), 0, st, A, lda, B, S, Z, B2, S2, Z2, C, ldc, M, N, K, g,
-                       part);
+                       part, grp);
   else if constexpr (!ROWS)
     hipLaunchKernelGGL((k_prefill2<INT4, WM, WN, RB, CW, false, ACT>), grid, dim3(WM * WN * 64),
-                       0, st, A, lda, B, S, Z, B2, S2, Z2, C, ldc, M, N, K, g, part);
+                       0, st, A, lda, B, S, Z, B2, S2, Z2, C, ldc, M, N, K, g, part, grp);
   MM_CHECK_LAUNCH("gemm(prefill2)");
   if (ks > 1) {
     const int OW = ACT == SK_PLAIN ? N : (ACT == SK_SWIGLU ? N : 2 * N);

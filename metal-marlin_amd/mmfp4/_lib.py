@@ -59,8 +59,6 @@ SIGNATURES: dict[str, tuple] = {
     "mm_fp4_flat_quantize": (_c_int, [_vp, _c_size, _c_int, _c_int, _vp, _vp, _vp]),
     "mm_fp4_flat_dequantize": (_c_int, [_vp, _vp, _c_size, _c_size, _c_int, _vp, _vp]),
     "mm_fp4_pack_pair": (_c_int, [_vp, _vp, _c_size, _vp, _vp]),
-    "mm_stream_read": (_c_int, [_vp, _c_size, _vp, _c_size, _vp]),
-    "mm_mfma_ceiling": (_c_int, [_vp, _vp, _c_size, _c_int, _vp, _c_size, _vp]),
 }
 
 _lib = None

@@ -84,6 +84,16 @@ DENSE = [
     (300, 2048, 1000, 64, "k_prefill2 ragged"),
     (100, 520, 260, 8, "k_prefill (N % 8, K % 64)"),
     (40, 200, 96, 8, "k_prefill (K % 64)"),
+    # every tile shape bench.py times, at its full size: config 2 (M = 8, 32)
+    # on the four Llama-3-8B layers, config 4 (M = 512, 2048) on both GEMMs
+    (8, 4096, 6144, 128, "config 2 qkv M=8"),
+    (8, 4096, 28672, 128, "config 2 gate_up M=8"),
+    (8, 14336, 4096, 128, "config 2 down M=8"),
+    (32, 4096, 4096, 128, "config 2 o M=32"),
+    (32, 4096, 28672, 128, "config 2 gate_up M=32"),
+    (512, 14336, 4096, 128, "config 4 down M=512"),
+    (2048, 4096, 14336, 128, "config 4 up M=2048 (256x256 tiles, two rounds)"),
+    (2048, 14336, 4096, 128, "config 4 down M=2048 (128x256 tiles over K=14336)"),
 ]
 
 
@@ -98,7 +108,12 @@ def test_fp4_gemm_bit_exact(rng, M, K, N, g, family):
 
 
 @pytest.mark.parametrize("M,K,N,g,family", [d for d in DENSE if d[0] in (1, 12, 13, 24, 32, 64,
-                                                                          128, 100)])
+                                                                          128, 100)]
+                         + [(16, 4096, 6144, 128, "config 3 qkv M=16"),
+                            (16, 4096, 4096, 128, "config 3 o M=16"),
+                            (16, 4096, 28672, 128, "config 3 gate_up M=16"),
+                            (16, 14336, 4096, 128, "config 3 down M=16"),
+                            (2048, 14336, 4096, 128, "INT4 prefill M=2048")])
 def test_u4_gemm_bit_exact(rng, M, K, N, g, family):
     import mmfp4
     packed, s, z = _exact_u4(rng, K, N, g)
@@ -106,6 +121,23 @@ def test_u4_gemm_bit_exact(rng, M, K, N, g, family):
     ref = ofp4.gemm_u4_ref(a, packed, s, z, g)
     announce(f"exact u4 {family} M={M} K={K} N={N} g={g}")
     _same(mmfp4.marlin_gemm_int4(to_dev(a), to_dev(packed), to_dev(s), to_dev(z), g), ref)
+
+
+@pytest.mark.parametrize("K,N", [(4096, 14336), (14336, 4096)])
+def test_fp4_gemm_bit_exact_m8192_rows(rng, K, N):
+    """Config 4 at M = 8192 (256x256 tiles for both GEMMs): the whole output
+    is computed on the GPU, and one seeded row of every 32-row block (so every
+    row tile and every MFMA row block of it) is checked bit-exactly against the
+    oracle.  Output rows depend only on their own activation row."""
+    import mmfp4
+    M, g = 8192, 128
+    packed, scales = _exact_fp4(rng, K, N, g)
+    a = _acts(rng, M, K)
+    rows = np.arange(0, M, 32) + rng.integers(0, 32, M // 32)
+    ref = ofp4.gemm_fp4_ref(a[rows], packed, scales, g)
+    announce(f"exact fp4 config 4 M=8192 K={K} N={N} (row subset)")
+    out = mmfp4.marlin_gemm_fp4(to_dev(a), to_dev(packed), to_dev(scales), g)
+    _same(out[torch.from_numpy(rows).to(out.device)], ref)
 
 
 @pytest.mark.parametrize("M,K,N,g", [(1, 4096, 6144, 128), (1, 14336, 4096, 128),

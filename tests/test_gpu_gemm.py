@@ -221,37 +221,46 @@ def test_split_k_large_and_nonfinite_partials(M, K):
 
 
 def test_stream_read_measurement_aid():
-    """mm_stream_read reads and writes nothing; misaligned sizes are refused."""
-    from mmfp4 import _lib
+    """mm_stream_read (bench.py's read-ceiling aid, libmmfp4_bench.so) reads
+    and writes nothing in every order and load form; bad arguments are
+    refused."""
+    import bench_aids
     buf = torch.arange(1 << 18, dtype=torch.int32, device="cuda")
     sink = torch.zeros(8192 * 512, dtype=torch.int32, device="cuda")
     st = torch.cuda.current_stream().cuda_stream
-    _lib.call("mm_stream_read", buf.data_ptr(), buf.numel() * 4, sink.data_ptr(), sink.numel() * 4, st)
+    for blocks, threads, unroll, mode in ((0, 0, 4, 1), (64, 256, 1, 0), (300, 1024, 16, 3),
+                                          (1000, 64, 8, 2)):
+        announce(f"stream read blocks={blocks} threads={threads} unroll={unroll} mode={mode}")
+        bench_aids.call("mm_stream_read", buf.data_ptr(), buf.numel() * 4, sink.data_ptr(),
+                        sink.numel() * 4, blocks, threads, unroll, mode, st)
     torch.cuda.synchronize()
     assert int(sink.abs().sum()) == 0
-    with pytest.raises(ValueError):
-        _lib.call("mm_stream_read", buf.data_ptr(), 1000, sink.data_ptr(), sink.numel() * 4, st)
+    for bad in ((1000, 0, 0, 4, 1), (4096, 64, 100, 4, 1), (4096, 64, 256, 3, 1),
+                (4096, 64, 256, 4, 4), (4096, 1 << 20, 1024, 4, 0)):
+        with pytest.raises(ValueError):
+            bench_aids.call("mm_stream_read", buf.data_ptr(), bad[0], sink.data_ptr(),
+                            sink.numel() * 4, *bad[1:], st)
 
 
 def test_mfma_ceiling_measurement_aid():
     """mm_mfma_ceiling's sums: with all-ones operands every accumulator gains
     16 per MFMA and 4 MFMAs per iteration, and a lane's 8 accumulators add to
     512 * iters; bad arguments are refused."""
-    from mmfp4 import _lib
+    import bench_aids
     ones = torch.ones(4096, dtype=torch.float16, device="cuda")
     sink = torch.zeros(256 * 512, dtype=torch.float32, device="cuda")
     st = torch.cuda.current_stream().cuda_stream
     announce("mfma ceiling iters=3")
-    _lib.call("mm_mfma_ceiling", ones.data_ptr(), ones.data_ptr(), ones.numel(), 3,
-              sink.data_ptr(), sink.numel() * 4, st)
+    bench_aids.call("mm_mfma_ceiling", ones.data_ptr(), ones.data_ptr(), ones.numel(), 3,
+                    sink.data_ptr(), sink.numel() * 4, st)
     torch.cuda.synchronize()
     assert torch.all(sink == 512 * 3)
     with pytest.raises(ValueError):
-        _lib.call("mm_mfma_ceiling", ones.data_ptr(), ones.data_ptr(), 12, 3, sink.data_ptr(),
-                  sink.numel() * 4, st)
+        bench_aids.call("mm_mfma_ceiling", ones.data_ptr(), ones.data_ptr(), 12, 3,
+                        sink.data_ptr(), sink.numel() * 4, st)
     with pytest.raises(ValueError):
-        _lib.call("mm_mfma_ceiling", ones.data_ptr(), ones.data_ptr(), 4096, 3, sink.data_ptr(),
-                  1024, st)
+        bench_aids.call("mm_mfma_ceiling", ones.data_ptr(), ones.data_ptr(), 4096, 3,
+                        sink.data_ptr(), 1024, st)
 
 
 @pytest.mark.parametrize("M,K,N,g,int4", [(1, 512, 3072, 128, False), (8, 4160, 3076, 64, False),
