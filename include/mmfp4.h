@@ -49,6 +49,23 @@ int mm_u4_dequant(const uint32_t* B, const uint16_t* scales, const uint16_t* zer
 int mm_fp4_quantize(const void* W, int w_is_f32, int N, int K, int group_size, uint32_t* B,
                     uint16_t* scales, void* stream);
 
+/* Calibration-aware FP4 quantizer (the activation_ranges branch of
+ * metal_marlin/quantize_fp4.py:205-256), same layouts as mm_fp4_quantize.
+ * The host passes the constants numpy would derive from the calibration dict:
+ *   use_pct, kprev, knext, gamma  percentile group max: numpy's 'linear'
+ *                  interpolation between the kprev-th and knext-th smallest
+ *                  |w| of a group with float32 weight gamma (use_pct 0: absmax)
+ *   mode           0: no input range; 1: act > 1, float32 blend
+ *                  c1 * gmax + c2 * gmax (c1 = f32(1 - sf), c2 = f32(sf));
+ *                  2: act <= 1, float64 blend f32(c1 * gmax) + sf * gmax * att,
+ *                  att = sqrt(act), and a float64 scale division
+ * Scales are fp16(group max / 6), codes the nearest E2M1 of
+ * w / f32(group max) * 6. */
+int mm_fp4_quantize_calibrated(const void* W, int w_is_f32, int N, int K, int group_size,
+                               int use_pct, int kprev, int knext, float gamma, int mode,
+                               float c1, float c2, double sf, double att, uint32_t* B,
+                               uint16_t* scales, void* stream);
+
 /* Asymmetric INT4 quantizer from W[N,K] fp16 into B, scales, zeros.
  * Replaces metal_marlin/metal_marlin.py:184-280 (pack_u4_weights). */
 int mm_u4_quantize(const uint16_t* W, int N, int K, int group_size, uint32_t* B,

@@ -71,6 +71,9 @@ k_u4_dequant(const uint32_t* __restrict__ B, const f16* __restrict__ S,
 // ---------------------------------------------------------------------------
 MM_DEV uint32_t e2m1_nearest(float v) {
   const float T[8] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f};
+  // NaN: np.clip keeps it and argmin over all-NaN distances picks index 0 of
+  // the negative table (NaN >= 0 is false): code 8.
+  if (v != v) return 8u;
   const bool neg = !(v >= 0.0f);
   // np.clip(v, lo, hi) == minimum(maximum(v, lo), hi)
   const float c = neg ? fminf(fmaxf(v, -6.0f), 0.0f) : fminf(fmaxf(v, 0.0f), 6.0f);
@@ -98,9 +101,15 @@ k_fp4_quantize(const T* __restrict__ Wt, int N, int K, int g,
   const int gi = blockIdx.y;
   if (n >= N) return;
   const T* row = Wt + (size_t)n * K + (size_t)gi * g;
+  // np.max and np.maximum propagate NaN (fmaxf would drop it).
   float amax = 0.0f;
-  for (int k = 0; k < g; ++k) amax = fmaxf(amax, fabsf(ld_f32(row + k)));
-  amax = fmaxf(amax, 1e-7f);
+  bool nan = false;
+  for (int k = 0; k < g; ++k) {
+    const float a = fabsf(ld_f32(row + k));
+    nan |= a != a;
+    amax = fmaxf(amax, a);
+  }
+  amax = nan ? __builtin_nanf("") : fmaxf(amax, 1e-7f);
   S[(size_t)gi * N + n] = (f16)(amax / 6.0f);
   const int wpg = g / 8;
   for (int w8 = 0; w8 < wpg; ++w8) {
@@ -108,6 +117,110 @@ k_fp4_quantize(const T* __restrict__ Wt, int N, int K, int g,
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const float v = ld_f32(row + 8 * w8 + i) / amax * 6.0f;
+      word |= e2m1_nearest(v) << (4 * i);
+    }
+    B[((size_t)gi * wpg + w8) * N + n] = word;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Calibration-aware FP4 quantizer: the activation_ranges branch of
+// quantize_fp4.py:205-256, in numpy's own arithmetic (the host derives the
+// constants the way numpy does):
+//   group max   np.percentile(|w|, p) ('linear': order statistics kprev and
+//               knext of the group's |w|, numpy's _lerp in float32 with
+//               weight gamma) when use_pct, else the absmax; a NaN in the
+//               group gives NaN (numpy sorts NaN last and flags the slice);
+//               then max(., f32(1e-7))
+//   mode 0      group max as is (no input range)
+//   mode 1      act > 1: f32(c1 * gmax) + f32(c2 * gmax), c1 = f32(1 - sf),
+//               c2 = f32(sf)
+//   mode 2      act <= 1: the calibrated max gmax * sqrt(act) is a float64
+//               product, so the blend f32(c1 * gmax) + sf * (gmax * att) and
+//               the scale's division by 6 run in float64, and the scale is the
+//               float64 quotient rounded once to fp16
+//   codes       nearest E2M1 of w / f32(group max) * 6, as the weight-only path
+// ---------------------------------------------------------------------------
+struct FqCal {
+  int use_pct, kprev, knext;
+  float gamma;
+  int mode;
+  float c1, c2;
+  double sf, att;
+};
+
+// k-th smallest (0-based) of |row[0..g)| by rank counting (offline, g^2).
+template <typename T>
+MM_DEV float kth_abs(const T* row, int g, int k) {
+  for (int i = 0; i < g; ++i) {
+    const float v = fabsf(ld_f32(row + i));
+    int less = 0, eq = 0;
+    for (int j = 0; j < g; ++j) {
+      const float a = fabsf(ld_f32(row + j));
+      less += a < v;
+      eq += a == v;
+    }
+    if (less <= k && k < less + eq) return v;
+  }
+  return __builtin_nanf("");
+}
+
+// fp16 of a float64 value, rounded once: round to float with the sticky bit
+// kept in the last place (round-to-odd), then float -> fp16 to nearest even.
+// Round-to-odd to 24 bits followed by a rounding to 11 bits is the correctly
+// rounded result (the intermediate has more than 2 extra bits).
+MM_DEV f16 f16_from_f64(double d) {
+  float f = (float)d;
+  if ((double)f != d && f == f) {
+    uint32_t b = __builtin_bit_cast(uint32_t, f);
+    if (fabs((double)f) > fabs(d)) b -= 1;     // back toward zero (truncation)
+    f = __builtin_bit_cast(float, b | 1u);
+  }
+  return (f16)f;
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256)
+k_fp4_quantize_cal(const T* __restrict__ Wt, int N, int K, int g, FqCal cal,
+                   uint32_t* __restrict__ B, f16* __restrict__ S) {
+  const int n = blockIdx.x * 256 + threadIdx.x;
+  const int gi = blockIdx.y;
+  if (n >= N) return;
+  const T* row = Wt + (size_t)n * K + (size_t)gi * g;
+  float amax = 0.0f;
+  bool nan = false;
+  for (int k = 0; k < g; ++k) {
+    const float a = fabsf(ld_f32(row + k));
+    nan |= a != a;
+    amax = fmaxf(amax, a);
+  }
+  float gmw = amax;
+  if (nan) {
+    gmw = __builtin_nanf("");
+  } else if (cal.use_pct) {
+    const float a = kth_abs(row, g, cal.kprev);
+    const float b = cal.knext == cal.kprev ? a : kth_abs(row, g, cal.knext);
+    const float diff = b - a;
+    gmw = cal.gamma >= 0.5f ? b - diff * (1.0f - cal.gamma) : a + diff * cal.gamma;
+  }
+  gmw = gmw != gmw ? gmw : fmaxf(gmw, 1e-7f);    // np.maximum propagates NaN
+  float gmf;
+  f16 scale;
+  if (cal.mode == 2) {
+    const double gm = (double)(cal.c1 * gmw) + cal.sf * ((double)gmw * cal.att);
+    scale = f16_from_f64(gm / 6.0);
+    gmf = (float)gm;
+  } else {
+    gmf = cal.mode == 1 ? cal.c1 * gmw + cal.c2 * gmw : gmw;
+    scale = (f16)(gmf / 6.0f);
+  }
+  S[(size_t)gi * N + n] = scale;
+  const int wpg = g / 8;
+  for (int w8 = 0; w8 < wpg; ++w8) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float v = ld_f32(row + 8 * w8 + i) / gmf * 6.0f;
       word |= e2m1_nearest(v) << (4 * i);
     }
     B[((size_t)gi * wpg + w8) * N + n] = word;
@@ -190,6 +303,27 @@ extern "C" int mm_fp4_quantize(const void* W, int w_is_f32, int N, int K, int g,
     hipLaunchKernelGGL(k_fp4_quantize<f16>, grid, dim3(256), 0, (hipStream_t)stream,
                        (const f16*)W, N, K, g, B, (f16*)S);
   MM_CHECK_LAUNCH("mm_fp4_quantize");
+  return 0;
+}
+
+extern "C" int mm_fp4_quantize_calibrated(const void* W, int w_is_f32, int N, int K, int g,
+                                          int use_pct, int kprev, int knext, float gamma,
+                                          int mode, float c1, float c2, double sf, double att,
+                                          uint32_t* B, uint16_t* S, void* stream) {
+  if (int rc = check_dims("mm_fp4_quantize_calibrated", K, N, g)) return rc;
+  MM_CHECK_ARG(!use_pct || (kprev >= 0 && kprev < g && knext >= kprev && knext < g),
+               "mm_fp4_quantize_calibrated: order statistics %d, %d outside a group of %d",
+               kprev, knext, g);
+  MM_CHECK_ARG(mode >= 0 && mode <= 2, "mm_fp4_quantize_calibrated: mode must be 0, 1 or 2");
+  const FqCal cal{use_pct != 0, kprev, knext, gamma, mode, c1, c2, sf, att};
+  dim3 grid(mm_cdiv(N, 256), K / g);
+  if (w_is_f32)
+    hipLaunchKernelGGL(k_fp4_quantize_cal<float>, grid, dim3(256), 0, (hipStream_t)stream,
+                       (const float*)W, N, K, g, cal, B, (f16*)S);
+  else
+    hipLaunchKernelGGL(k_fp4_quantize_cal<f16>, grid, dim3(256), 0, (hipStream_t)stream,
+                       (const f16*)W, N, K, g, cal, B, (f16*)S);
+  MM_CHECK_LAUNCH("mm_fp4_quantize_calibrated");
   return 0;
 }
 

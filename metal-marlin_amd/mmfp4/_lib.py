@@ -23,6 +23,10 @@ SIGNATURES: dict[str, tuple] = {
     "mm_fp4_dequant": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _vp]),
     "mm_u4_dequant": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp]),
     "mm_fp4_quantize": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp]),
+    "mm_fp4_quantize_calibrated": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
+                                            _c_int, ctypes.c_float, _c_int, ctypes.c_float,
+                                            ctypes.c_float, ctypes.c_double, ctypes.c_double,
+                                            _vp, _vp, _vp]),
     "mm_u4_quantize": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp]),
     "mm_gemm_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int]),
     "mm_fp4_gemm": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _c_size,

@@ -48,12 +48,12 @@ def quantize_fp4(weight, group_size: int = 128, activation_ranges=None,
                  marlin_layout: bool = True):
     """Quantize W [out_features, in_features] to FP4 E2M1, Marlin layout:
     (packed [K/8, N] uint32, scales [K/group_size, N] fp16).
-    quantize_fp4.py:131-284 (weight-only path)."""
+    quantize_fp4.py:131-284; with activation_ranges ({"percentile",
+    "smooth_factor", "input_range"}) the calibration-aware group maxima of
+    :205-256 (percentile clip, sqrt(act) attenuation for act <= 1, blend),
+    bit-identical to the reference's numpy arithmetic."""
     if not marlin_layout:
         raise ValueError("Legacy layout is not supported. Use marlin_layout=True.")
-    if activation_ranges is not None:
-        raise NotImplementedError(
-            "calibration-aware scaling (activation_ranges) is not part of this library")
     w, from_np = _to_device(weight)
     if w.dtype not in (torch.float16, torch.float32):
         w = w.to(torch.float32)
@@ -64,9 +64,56 @@ def quantize_fp4(weight, group_size: int = 128, activation_ranges=None,
         raise ValueError(f"Pack axis ({K}) must be divisible by group_size ({group_size})")
     packed = torch.empty((K // 8, N), dtype=torch.int32, device=w.device)
     scales = torch.empty((K // group_size, N), dtype=torch.float16, device=w.device)
-    _lib.call("mm_fp4_quantize", _lib.ptr(w), int(w.dtype == torch.float32), N, K, group_size,
-              _lib.ptr(packed), _lib.ptr(scales), _lib.stream_of(w))
+    if activation_ranges is None:
+        _lib.call("mm_fp4_quantize", _lib.ptr(w), int(w.dtype == torch.float32), N, K,
+                  group_size, _lib.ptr(packed), _lib.ptr(scales), _lib.stream_of(w))
+    else:
+        c = _calibration_constants(activation_ranges, group_size)
+        _lib.call("mm_fp4_quantize_calibrated", _lib.ptr(w), int(w.dtype == torch.float32), N, K,
+                  group_size, *c, _lib.ptr(packed), _lib.ptr(scales), _lib.stream_of(w))
     return _out(packed, from_np, np.uint32), _out(scales, from_np)
+
+
+def _calibration_constants(activation_ranges, group_size: int) -> tuple:
+    """The constants numpy derives from the calibration dict in the
+    reference's activation_ranges branch (quantize_fp4.py:205-256), for
+    mm_fp4_quantize_calibrated: (use_pct, kprev, knext, gamma, mode, c1, c2,
+    sf, att).
+
+    * np.percentile(|w|, p, axis=group) ('linear'): q = f32(p) / f32(100),
+      index vi = (g - 1) * q in float32, neighbours floor(vi) and floor(vi) + 1
+      (both the last when vi >= g - 1, where numpy's gamma is vi + 1);
+    * (1.0 - sf) and sf meet a float32 array as Python floats (float32 ops);
+      np.sqrt(act) is a float64 scalar, which makes the act <= 1 blend float64.
+    "percentile", "smooth_factor" and the range ends are read as Python
+    numbers."""
+    pct = float(activation_ranges.get("percentile", 100.0))
+    sf = float(activation_ranges.get("smooth_factor", 1.0))
+    if not 0.0 <= pct <= 100.0:
+        raise ValueError("Percentiles must be in the range [0, 100]")
+    use_pct, kprev, knext, gamma = 0, 0, 0, 0.0
+    if pct < 100.0:
+        use_pct = 1
+        q = np.true_divide(pct, np.float32(100))
+        vi = np.float32((group_size - 1) * q)
+        prev = np.floor(vi)
+        if vi >= group_size - 1:
+            kprev = knext = group_size - 1
+            gamma = float(vi - np.float32(-1))
+        else:
+            kprev, knext = int(prev), int(prev) + 1
+            gamma = float(vi - prev)
+    input_range = activation_ranges.get("input_range")
+    mode, att = 0, 1.0
+    if input_range is not None:
+        a_min, a_max = input_range
+        act = max(abs(float(a_min)), abs(float(a_max)))
+        if act > 1.0:
+            mode = 1
+        else:
+            mode, att = 2, float(np.sqrt(act))
+    c1, c2 = float(np.float32(1.0 - sf)), float(np.float32(sf))
+    return use_pct, kprev, knext, gamma, mode, c1, c2, sf, att
 
 
 def unpack_fp4(packed, scales, group_size: int = 128, marlin_layout: bool | None = None):

@@ -19,6 +19,13 @@ Pinning status (what checks each function against something other than itself):
 * `quantize_fp4`                 -- pinned: golden vectors written by importing
   the reference's quantize_fp4.py (tests/golden/make_quantize_fp4_vectors.py),
   plus the nearest-value invariant on random and crafted midpoint inputs.
+* `quantize_fp4_calibrated`      -- pinned (tests/test_oracle_quant_cal.py):
+  golden vectors of the reference's activation_ranges branch (same script),
+  the percentile against an exact-rational order-statistic brute force,
+  smooth_factor = 0 and percentile = 100 reducing to the weight-only
+  quantizer, act <= 1 scaling the group max by sqrt(act) (exact at act = 1/4
+  and 1/16), the float64 scale rounding against a Fraction closed form, and
+  the nearest-value invariant of the codes.
 * `pack_u4_weights`              -- pinned (tests/test_oracle_pin.py): a
   float64 nearest-integer brute force of q away from ties, crafted groups
   where the float32 scale and its fp16 rounding give different q, exact .5

@@ -123,6 +123,50 @@ def quantize_fp4(weight: np.ndarray, group_size: int = 128):
     return pack_nibbles(quantize_to_fp4(w_scaled)), scales
 
 
+def quantize_fp4_calibrated(weight: np.ndarray, group_size: int,
+                            activation_ranges: dict):
+    """Calibration-aware FP4 quantizer, Marlin layout: the activation_ranges
+    branch of quantize_fp4.py:205-256, with numpy's own dtype flow (NEP 50):
+
+    * group max: np.percentile(|w|, p) over the group when p < 100 (numpy's
+      'linear' method on float32), else the absmax; floored at 1e-7 (f32);
+    * with "input_range" (a_min, a_max), act = max(|a_min|, |a_max|):
+      act > 1  -> calibrated = group max, blended in float32:
+                  (1 - sf) * gmax + sf * calibrated;
+      act <= 1 -> calibrated = gmax * np.sqrt(act), a float64 scalar, so the
+                  blend (and the scale's division by 6) runs in float64;
+    * scales = fp16(group_max / 6); codes = nearest E2M1 of w / f32(group_max) * 6.
+
+    "percentile", "smooth_factor" and the range ends are taken as Python
+    numbers (the reference's defaults 100.0 and 1.0).
+    """
+    pct = float(activation_ranges.get("percentile", 100.0))
+    sf = float(activation_ranges.get("smooth_factor", 1.0))
+    input_range = activation_ranges.get("input_range")
+    w = np.asarray(weight).astype(np.float32).T
+    k, n = w.shape
+    if k % 8 != 0:
+        raise ValueError(f"Pack axis ({k}) must be divisible by 8")
+    if k % group_size != 0:
+        raise ValueError(f"Pack axis ({k}) must be divisible by group_size ({group_size})")
+    g = w.reshape(k // group_size, group_size, n)
+    if pct < 100.0:
+        gmw = np.percentile(np.abs(g), pct, axis=1, keepdims=True)
+    else:
+        gmw = np.max(np.abs(g), axis=1, keepdims=True)
+    gmw = np.maximum(gmw, 1e-7)
+    if input_range is not None:
+        a_min, a_max = input_range
+        act = max(abs(float(a_min)), abs(float(a_max)))
+        cal = gmw if act > 1.0 else gmw * np.sqrt(act)
+        gmax = (1.0 - sf) * gmw + sf * cal
+    else:
+        gmax = gmw
+    scales = (gmax / 6.0).astype(np.float16).squeeze(1)
+    w_scaled = (g / gmax.astype(np.float32) * 6.0).reshape(k, n)
+    return pack_nibbles(quantize_to_fp4(w_scaled)), scales
+
+
 def pack_u4_weights(weight: np.ndarray, group_size: int = 128):
     """Asymmetric INT4 quantizer, Marlin layout.  metal_marlin.py:184-280:
     w = fp16(W).T as f32; per group s = max((max-min)/15, 1e-7) (f32),
