@@ -277,8 +277,12 @@ def run_host_paced(torch, mmfp4, n: int = 400):
 
 def run_layer_graph(torch, mmfp4, n: int):
     """The four Llama-layer GEMMs at M=1 host-paced, eager (four library calls
-    per step) and as one captured HIP graph replayed per step: wall µs per
-    step over n back-to-back steps (same weights every step)."""
+    per step), as one captured HIP graph of one step replayed per step, and as
+    one graph of ten steps: wall µs per step over back-to-back steps (same
+    weights every step), plus the GPU-side time per step with the launches
+    queued behind a GPU sleep (no host pacing).  A replay costs a fixed gap on
+    the GPU between consecutive graph launches; kernels inside a graph run at
+    their eager durations, so longer graphs amortise it."""
     ws = [make_weights(torch, mmfp4, K, N, 820 + i) for i, (_, K, N) in enumerate(LLAMA_LAYER)]
     xs = {K: torch.randn((1, K), device="cuda").half() for _, K, _ in LLAMA_LAYER}
 
@@ -286,17 +290,19 @@ def run_layer_graph(torch, mmfp4, n: int):
         return [mmfp4.marlin_gemm_fp4(xs[K], w[0], w[1], G)
                 for (_, K, _), w in zip(LLAMA_LAYER, ws)]
 
-    def wall(fn):
+    def wall(fn, reps, per):
         for _ in range(10):
             fn()
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        for _ in range(n):
+        for _ in range(reps):
             fn()
         torch.cuda.synchronize()
-        return 1e6 * (time.perf_counter() - t0) / n
+        w = 1e6 * (time.perf_counter() - t0) / (reps * per)
+        gpu = 1e3 * timed_launches(torch, [[fn]], reps, 2) / (reps * per)
+        return round(w, 2), round(gpu, 2)
 
-    eager = wall(step)
+    eager = wall(step, n, 1)
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
@@ -304,11 +310,18 @@ def run_layer_graph(torch, mmfp4, n: int):
         step()
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g, stream=s):
+    g1, g10 = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g1, stream=s):
         step()
-    graph = wall(g.replay)
-    return {"eager_wall_us_per_step": round(eager, 2), "graph_wall_us_per_step": round(graph, 2),
+    with torch.cuda.graph(g10, stream=s):
+        for _ in range(10):
+            step()
+    graph = wall(g1.replay, n, 1)
+    graph10 = wall(g10.replay, max(5, n // 10), 10)
+    return {"eager_wall_us_per_step": eager[0], "eager_gpu_us_per_step": eager[1],
+            "graph_wall_us_per_step": graph[0], "graph_gpu_us_per_step": graph[1],
+            "graph_of_10_steps_wall_us_per_step": graph10[0],
+            "graph_of_10_steps_gpu_us_per_step": graph10[1],
             "launches_per_step": len(LLAMA_LAYER)}
 
 
@@ -583,7 +596,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--all", action="store_true", help="accepted for compatibility; every "
                     "BASELINE config is reported by default")
-    ap.add_argument("--section", choices=("all", "layer", "prefill", "moe", "fused"),
+    ap.add_argument("--section", choices=("all", "layer", "prefill", "moe", "fused", "graph"),
                     default="all",
                     help="run one workload alone (for profiling); the default runs all and "
                          "prints the contract line")
@@ -617,6 +630,8 @@ def main() -> int:
             tf = r["flops"] / (r["ms_per_step"] * 1e-3) / 1e12
             res = {"ms_per_step": round(r["ms_per_step"], 4), "per_shape": r["per_shape"],
                    "TFLOPs": round(tf, 1), "mfma_ceiling": run_mfma_ceiling(torch, mmfp4, tf)}
+        elif args.section == "graph":
+            res = run_layer_graph(torch, mmfp4, 200)
         elif args.section == "moe":
             res = [run_moe_bench(torch, mmfp4, T, 20) for T in (32, 1024)]
         else:

@@ -18,18 +18,34 @@ namespace {
 std::mutex g_mu;
 std::map<std::pair<int, int64_t>, at::Tensor> g_ws;   // (device index, stream) -> workspace
 
-at::Tensor workspace(const at::Tensor& like, int64_t stream, size_t nbytes) {
+// One workspace per (device, stream), shared with the ctypes path (which
+// asks for it through workspace_for below); kept until release_workspaces().
+at::Tensor workspace_dev(int dev, int64_t stream, size_t nbytes, const at::TensorOptions& opt) {
   std::lock_guard<std::mutex> lock(g_mu);
-  const auto key = std::make_pair((int)like.get_device(), stream);
+  const auto key = std::make_pair(dev, stream);
   auto it = g_ws.find(key);
   if (it != g_ws.end() && (size_t)it->second.numel() >= nbytes) return it->second;
   size_t size = nbytes < ((size_t)1 << 20) ? ((size_t)1 << 20) : nbytes;
   if (it != g_ws.end() && size < 2 * (size_t)it->second.numel()) size = 2 * it->second.numel();
   // Zero-filled once: the split-K arrival counters at its head must start at
   // zero, and every call leaves them at zero.
-  at::Tensor buf = at::zeros({(int64_t)size}, like.options().dtype(at::kByte));
+  at::Tensor buf = at::zeros({(int64_t)size}, opt.dtype(at::kByte));
   g_ws[key] = buf;
   return buf;
+}
+
+at::Tensor workspace(const at::Tensor& like, int64_t stream, size_t nbytes) {
+  return workspace_dev((int)like.get_device(), stream, nbytes, like.options());
+}
+
+at::Tensor workspace_for(int64_t device, int64_t stream, int64_t nbytes) {
+  return workspace_dev((int)device, stream, (size_t)nbytes,
+                       at::TensorOptions().device(at::kCUDA, (int)device));
+}
+
+void release_workspaces() {
+  std::lock_guard<std::mutex> lock(g_mu);
+  g_ws.clear();
 }
 
 [[noreturn]] void fail(int rc) {
@@ -112,4 +128,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("gemm", &gemm, "C = A . dequant(B, S[, Z]) on the given stream", pybind11::arg("A"),
         pybind11::arg("B"), pybind11::arg("S"), pybind11::arg("Z"),
         pybind11::arg("group_size"), pybind11::arg("stream"));
+  m.def("workspace", &workspace_for,
+        "the zero-initialised workspace of (device index, raw stream), at least nbytes",
+        pybind11::arg("device"), pybind11::arg("stream"), pybind11::arg("nbytes"));
+  m.def("release_workspaces", &release_workspaces, "drop every cached workspace");
 }

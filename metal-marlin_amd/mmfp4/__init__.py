@@ -31,4 +31,6 @@ from .quantized_linear import (KernelLibrary, MarlinLinear, QuantizedLinear, Qua
                                dequant_fp4_bulk, dequant_int4_bulk, get_default_library,
                                quantized_linear)
 
+from ._lib import release_workspaces
+
 __version__ = "0.1.0"

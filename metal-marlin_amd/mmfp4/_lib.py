@@ -136,6 +136,27 @@ def call(name: str, *args) -> None:
     check(getattr(F, name)(*args))
 
 
+def derived(src: torch.Tensor, key: str, build) -> torch.Tensor:
+    """build(src), cached on the tensor object `src` under `key` and rebuilt
+    when src is written in place (its version counter) or points at other
+    storage.  The copy lives exactly as long as the source tensor object; a
+    caller that passes a fresh view each time gets no caching."""
+    cache = getattr(src, "_mmfp4_derived", None)
+    stamp = (src._version, src.data_ptr(), tuple(src.shape), src.dtype)
+    hit = cache.get(key) if cache is not None else None
+    if hit is not None and hit[0] == stamp:
+        return hit[1]
+    out = build(src)
+    if cache is None:
+        cache = {}
+        try:
+            src._mmfp4_derived = cache
+        except (AttributeError, RuntimeError):
+            return out
+    cache[key] = (stamp, out)
+    return out
+
+
 def ptr(t: torch.Tensor | None) -> ctypes.c_void_p:
     return ctypes.c_void_p(0 if t is None else t.data_ptr())
 
@@ -202,7 +223,13 @@ _ws: dict[tuple[int, int], torch.Tensor] = {}
 
 
 def workspace_on(index: int, stream: int, nbytes: int) -> torch.Tensor:
-    """Workspace of at least `nbytes` for (device index, raw stream)."""
+    """Workspace of at least `nbytes` for (device index, raw stream): one
+    zero-initialised buffer per pair (at least 1 MiB, grown by doubling),
+    held by the per-call binding when it is built (so both call paths share
+    it), else here.  Buffers are kept until release_workspaces()."""
+    b = binding()
+    if b:
+        return b.workspace(index, stream, nbytes)
     key = (index, stream)
     buf = _ws.get(key)
     if buf is None or buf.numel() < nbytes:
@@ -212,6 +239,17 @@ def workspace_on(index: int, stream: int, nbytes: int) -> torch.Tensor:
         buf = torch.zeros(size, dtype=torch.uint8, device=torch.device("cuda", index))
         _ws[key] = buf
     return buf
+
+
+def release_workspaces() -> None:
+    """Drop every cached workspace (for callers that create and destroy many
+    streams: one buffer per stream is otherwise kept for the process).  Call
+    it once the work queued on those streams has finished; a captured HIP
+    graph that used a released workspace must not be replayed afterwards."""
+    b = binding()
+    if b:
+        b.release_workspaces()
+    _ws.clear()
 
 
 def workspace(device: torch.device, nbytes: int) -> torch.Tensor:

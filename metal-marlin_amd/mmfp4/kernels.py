@@ -59,11 +59,17 @@ def _gemm(kind: str, A: torch.Tensor, B_packed: torch.Tensor, scales: torch.Tens
         # lm_head over 32001 tokens, say) run on copies padded to a multiple
         # of 4 -- zero words, unit scales, zero points 0, so the extra columns
         # are exact zeros -- and return the first N columns.
+        # The padded copies are cached on the operand tensors themselves
+        # (rebuilt when a tensor is written in place or its storage changes),
+        # so repeated calls with the same weights pay the copy once.
         pad = (0, -N % 4)
-        zp = None if zeros is None else torch.nn.functional.pad(zeros, pad)
-        words = B_packed.view(torch.int32) if B_packed.dtype == torch.uint32 else B_packed
-        out = _gemm(kind, A, torch.nn.functional.pad(words, pad),
-                    torch.nn.functional.pad(scales, pad, value=1.0), zp, group_size)
+        F = torch.nn.functional
+        zp = None if zeros is None else _lib.derived(zeros, "pad4", lambda t: F.pad(t, pad))
+        words = _lib.derived(
+            B_packed, "pad4",
+            lambda t: F.pad(t.view(torch.int32) if t.dtype == torch.uint32 else t, pad))
+        sp = _lib.derived(scales, "pad4", lambda t: F.pad(t, pad, value=1.0))
+        out = _gemm(kind, A, words, sp, zp, group_size)
         return out[..., :N].contiguous()
     fast = _BINDING if _BINDING is not None else _binding()
     if fast:
@@ -269,7 +275,10 @@ def mmfp4_fused_gate_up(x: torch.Tensor, gate_packed: torch.Tensor, gate_scales:
     are transposed to the Marlin layout on the device for each call (as the
     reference's own M < 64 path does); callers that keep the Marlin layout
     call `mmfp4_fused_gate_up_marlin`.
-    SiLU is applied to the fp32 sums (the reference rounds them to fp16 first)."""
+    Rounding of the SiLU input depends on the path: the one-launch pair
+    kernels (N % 8 == 0, and K % 64 == 0 above 32 rows) apply SiLU to the
+    fp32 sums; the two-launch fallback for other shapes applies it to the
+    fp16-rounded products, which is the reference's own rounding."""
     if x.dim() != 2:
         raise ValueError(f"x must be 2D [M, K], got shape={tuple(x.shape)}")
     M, K = x.shape

@@ -107,6 +107,7 @@ class MMFP4Linear(nn.Module):
         self.register_buffer("scales", s)
         self.register_buffer("bias", None if bias is None else bias.contiguous())
         self.register_buffer("_kernel_packed_weights", None, persistent=False)
+        self.register_buffer("_kernel_scales", None, persistent=False)
         self.group_size = int(group_size)
         self.in_features = in_f
         self.out_features = out_f
@@ -140,16 +141,17 @@ class MMFP4Linear(nn.Module):
         if not x.is_floating_point():
             raise ValueError(f"x must be a floating tensor, got dtype={x.dtype}")
         x2 = x.reshape(-1, self.in_features)
-        scales = self.scales.to(x.device)
         if kernels.rowpacked_gemm_supported(x2.shape[0], self.out_features, self.in_features,
                                             self.group_size):
             # row-packed words and [n_groups, out] scales in place
-            out = kernels.mmfp4_gemm_rowpacked(x2, self.packed_weights.to(x.device), scales,
-                                               self.group_size)
+            out = kernels.mmfp4_gemm_rowpacked(x2, self.packed_weights.to(x.device),
+                                               self.scales.to(x.device), self.group_size)
         else:
             kp, ks = self._kernel_weights(x.device)
-            out = kernels.marlin_gemm_fp4(x2, kp, scales if ks is None else ks, self.group_size)
-            out = out[:, :self.out_features] if ks is not None else out
+            if ks is None:
+                out = kernels.marlin_gemm_fp4(x2, kp, self.scales.to(x.device), self.group_size)
+            else:
+                out = kernels.marlin_gemm_fp4(x2, kp, ks, self.group_size)[:, :self.out_features]
         if self.bias is not None:
             out = out + self.bias.to(device=out.device, dtype=out.dtype)
         out = out.reshape(*x.shape[:-1], self.out_features)

@@ -313,3 +313,40 @@ def test_binding_and_ctypes_paths_agree(M, K, N):
             fn(a, packed, scales, 64)
         with pytest.raises(RuntimeError, match="GPU only"):
             fn(a.cpu(), packed, scales, 128)
+
+
+def test_odd_width_padding_is_cached_on_the_operands(rng):
+    """N % 4 != 0: the padded copies are built once per operand tensor and
+    rebuilt after an in-place write (the version counter moves)."""
+    import mmfp4
+    K, N, g = 512, 1002, 128
+    w = rng.normal(0, 0.02, (N, K)).astype(np.float16)
+    packed, scales = ofp4.quantize_fp4(w, g)
+    a = rng.normal(0, 1, (3, K)).astype(np.float16)
+    dp, ds, da = to_dev(packed), to_dev(scales), to_dev(a)
+    announce("odd width padding cache")
+    out1 = mmfp4.marlin_gemm_fp4(da, dp, ds, g)
+    cached = dp._mmfp4_derived["pad4"][1]
+    out2 = mmfp4.marlin_gemm_fp4(da, dp, ds, g)
+    assert dp._mmfp4_derived["pad4"][1] is cached
+    assert torch.equal(out1, out2)
+    assert max_abs_rel(to_np(out1), ofp4.gemm_fp4_ref(a, packed, scales, g)) <= TOL
+    ds.mul_(2)                                   # in-place write: rebuilt, result doubles
+    out3 = mmfp4.marlin_gemm_fp4(da, dp, ds, g)
+    assert torch.equal(out3, (out1.float() * 2).half())
+
+
+def test_workspace_shared_between_call_paths_and_released():
+    from mmfp4 import _lib
+    import mmfp4
+    dev = torch.device("cuda", torch.cuda.current_device())
+    st = _lib.raw_stream(dev.index)
+    w1 = _lib.workspace_on(dev.index, st, 4096)
+    assert _lib.workspace(dev, 4096).data_ptr() == w1.data_ptr()
+    b = _lib.binding()
+    if b:
+        assert b.workspace(dev.index, st, 4096).data_ptr() == w1.data_ptr()
+    mmfp4.release_workspaces()
+    torch.cuda.synchronize()
+    w2 = _lib.workspace_on(dev.index, st, 4096)
+    assert int(w2[:65536].count_nonzero()) == 0       # fresh, zeroed counters
