@@ -123,6 +123,18 @@ int mm_u4_gemm(const uint16_t* A, const uint32_t* B, const uint16_t* scales,
                const uint16_t* zeros, uint16_t* C, int M, int N, int K, int group_size, void* ws,
                size_t ws_bytes, void* stream);
 
+/* mm_u4_gemm with the scales and zero points also given interleaved,
+ * SZ[K/g, N/4, 8] fp16 (16-byte aligned): for each 4-column group its 4
+ * scales then its 4 zero points.  The decode kernels (M <= 32) then load one
+ * 16-byte piece per group instead of two 8-byte ones; the prefill kernels read
+ * S and Z.  Results are bit-identical to mm_u4_gemm.  Replaces the same
+ * reference interface as mm_u4_gemm (kernels_core.py:1959-2066); the
+ * interleaved copy is a layout cache the Python layer keeps per (scales,
+ * zeros) pair. */
+int mm_u4_gemm_sz(const uint16_t* A, const uint32_t* B, const uint16_t* scales,
+                  const uint16_t* zeros, const uint16_t* SZ, uint16_t* C, int M, int N, int K,
+                  int group_size, void* ws, size_t ws_bytes, void* stream);
+
 /* Gate and up projections over two packed FP4 matrices (Marlin [K/8, N],
  * scales [K/g, N]) in one launch, reading A once:
  *   act = 1:  C[M, N]  = silu(A . dequant(Bg, Sg)) * (A . dequant(Bu, Su))

@@ -77,7 +77,7 @@ constexpr int sk_min_waves() {
              ? 4
              : 1;
 }
-template <bool INT4, int MT, int NT, int SPW, int NW, int FL, int ACT, int ROWP = 0>
+template <int INT4, int MT, int NT, int SPW, int NW, int FL, int ACT, int ROWP = 0>
 __global__ void __launch_bounds__(NW * 64, (sk_min_waves<ROWP, NT, FL>()))
 k_skinny(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
          const f16* __restrict__ S, const f16* __restrict__ Z, const uint32_t* __restrict__ B2,
@@ -280,7 +280,7 @@ k_skinny(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
 // ROWP: row-packed FP4 words [N, K/8] (K % 512 == 0), transposed through
 // LDS into the Marlin operand order (skinny_wave RT); scales [N, K/g] when
 // SROW, else [K/g, N].
-template <bool INT4, int SPW, int NW, int FL, bool SROW = false, bool ROWP = false>
+template <int INT4, int SPW, int NW, int FL, bool SROW = false, bool ROWP = false>
 __global__ void __launch_bounds__(NW * 64)
 k_skinny_dual(const f16* __restrict__ A, const uint32_t* __restrict__ B,
               const f16* __restrict__ S, const f16* __restrict__ Z, f16* __restrict__ C, int M,
@@ -328,7 +328,7 @@ k_skinny_dual(const f16* __restrict__ A, const uint32_t* __restrict__ B,
 
 // Column-strip kernel (M <= 16, group size a multiple of 32): one block per
 // NS*16 columns over the whole K; no split-K and no workspace.
-template <bool INT4, int NS, int SPW, int NW, int FL>
+template <int INT4, int NS, int SPW, int NW, int FL>
 __global__ void __launch_bounds__(NW * 64)
 k_strip(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
         const f16* __restrict__ S, const f16* __restrict__ Z, f16* __restrict__ C, int ldc,
@@ -755,7 +755,7 @@ size_t skinny_ws_bytes(int M, int N, int K) {
 // SK_MULTI: `mp` describes the matrices (N is then mp->ntot, B..Z2 unused).
 #define MM_ROWP_TILES 1      // 64-column tiles per block of the plain row-packed product; 2
                              // measured slower at M=1 (4096x6144 10.1 -> 18.8 us)
-template <bool INT4, int MT, int ACT, int ROWP = 0>
+template <int INT4, int MT, int ACT, int ROWP = 0>
 int launch_skinny(const f16* A, int lda, const uint32_t* B, const f16* S, const f16* Z,
                   const uint32_t* B2, const f16* S2, const f16* Z2, f16* C, int ldc, int M,
                   int N, int K, int g, void* ws, size_t ws_bytes, hipStream_t st,
@@ -803,7 +803,7 @@ int launch_skinny(const f16* A, int lda, const uint32_t* B, const f16* S, const 
 // Plain skinny product with two 64-column tiles per block and the whole K
 // range per block (no split, so no workspace is touched).  The caller
 // guarantees at least MM_SK_NOSPLIT_TILES blocks.
-template <bool INT4, int MT>
+template <int INT4, int MT>
 int launch_skinny_nt2(const f16* A, const uint32_t* B, const f16* S, const f16* Z, f16* C, int M,
                       int N, int K, int g, hipStream_t st) {
   constexpr int NT = 2, SPW = sk_spw<MT>(), NW = sk_nw<MT>();
@@ -848,7 +848,7 @@ bool use_dual(int M, int N, int K, int g) {
          mm_cdiv(N, SK_COLS) < MM_SK_DUAL_BELOW && mm_cdiv(N, 32) >= MM_SK_DUAL_MIN_TILES;
 }
 
-template <bool INT4, bool SROW = false>
+template <int INT4, bool SROW = false>
 int launch_dual(const f16* A, const uint32_t* B, const f16* S, const f16* Z, f16* C, int M, int N,
                 int K, int g, hipStream_t st) {
   constexpr int SPW = MM_SK_DUAL_SPW, NW = MM_SK_DUAL_NW;
@@ -877,7 +877,7 @@ int launch_dual(const f16* A, const uint32_t* B, const f16* S, const f16* Z, f16
 #define MM_ST_NW 8
 #define MM_ST_SPW 8
 
-template <bool INT4, int NS>
+template <int INT4, int NS>
 int launch_strip(const f16* A, int lda, const uint32_t* B, const f16* S, const f16* Z, f16* C,
                  int ldc, int M, int N, int K, int g, hipStream_t st) {
   constexpr int NW = MM_ST_NW, SPW = MM_ST_SPW;
@@ -987,43 +987,50 @@ int launch_prefill2(const f16* A, int lda, const uint32_t* B, const f16* S, cons
   return 0;
 }
 
-template <bool INT4>
+template <int INT4>
+// INT4 == 2: SZ holds the scales and zero points interleaved ([K/g, N/4, 8],
+// see load_sz4) for the decode kernels; the prefill kernels read S and Z.
 int gemm_dispatch(const char* who, const f16* A, const uint32_t* B, const f16* S, const f16* Z,
                   f16* C, int M, int N, int K, int g, void* ws, size_t ws_bytes,
-                  hipStream_t st) {
+                  hipStream_t st, const f16* SZ = nullptr) {
+  constexpr bool U4 = INT4 != 0;
+  // the decode kernels' scale operand: SZ for the interleaved form
+  const f16* Sd = INT4 == 2 ? SZ : S;
   MM_CHECK_ARG(M >= 0 && N > 0 && K > 0, "%s: bad shape M=%d N=%d K=%d", who, M, N, K);
   MM_CHECK_ARG(K % 8 == 0, "%s: K=%d must be divisible by 8", who, K);
   MM_CHECK_ARG(N % 4 == 0, "%s: N=%d must be divisible by 4", who, N);
   MM_CHECK_ARG(g > 0 && g % 8 == 0 && K % g == 0,
                "%s: group_size=%d must be a multiple of 8 dividing K=%d", who, g, K);
   MM_CHECK_ARG(((uintptr_t)A & 15) == 0 && ((uintptr_t)B & 15) == 0 && ((uintptr_t)S & 7) == 0 &&
-                   ((uintptr_t)C & 7) == 0 && (!INT4 || ((uintptr_t)Z & 7) == 0),
-               "%s: operands must be 16-byte (A, B) / 8-byte (scales, zeros, C) aligned", who);
+                   ((uintptr_t)C & 7) == 0 && (!INT4 || ((uintptr_t)Z & 7) == 0) &&
+                   (INT4 != 2 || ((uintptr_t)SZ & 15) == 0),
+               "%s: operands must be 16-byte (A, B, interleaved scales/zeros) / 8-byte "
+               "(scales, zeros, C) aligned", who);
   if (M == 0) return 0;
   // The decode kernels address one weight matrix with 32-bit byte offsets;
   // larger matrices take the prefill kernels (64-bit addressing) at any M.
   const bool off32 = (size_t)(K / 8) * (size_t)N * 4 < ((size_t)1 << 32);
-  if (off32 && use_dual(M, N, K, g)) return launch_dual<INT4>(A, B, S, Z, C, M, N, K, g, st);
+  if (off32 && use_dual(M, N, K, g)) return launch_dual<INT4>(A, B, Sd, Z, C, M, N, K, g, st);
   if (off32 && M <= 16 && flush_steps(g, MM_ST_SPW) > 0) {
     // Column strips (no split-K hand-off) win for small layers, where the
     // hand-off is a large share of the launch; split-K wins from ~13 MB up
     // (measured on MI355X: 4096x4096 5.8 vs 7.0 us, 4096x6144 8.0 vs 7.2 us).
     if ((long)K * N <= 4096L * 4096 && N / 16 >= 128)
-      return launch_strip<INT4, 1>(A, K, B, S, Z, C, N, M, N, K, g, st);
+      return launch_strip<INT4, 1>(A, K, B, Sd, Z, C, N, M, N, K, g, st);
   }
   // Wide layers at 9..32 rows: 128-column blocks (NT = 2) with no K split.  The
   // activation rows each block reads are then shared by twice the weight
   // columns (measured on MI355X, 4096 x 28672: M=16 16.5 -> 15.0 us, M=32
   // 24.6 -> 20.4 us; at M <= 8 and on narrower layers the 64-column plan wins).
   if (off32 && M > 8 && M <= 32 && mm_cdiv(N, 2 * SK_COLS) >= MM_SK_NOSPLIT_TILES) {
-    if (M <= 16) return launch_skinny_nt2<INT4, 1>(A, B, S, Z, C, M, N, K, g, st);
-    return launch_skinny_nt2<INT4, 2>(A, B, S, Z, C, M, N, K, g, st);
+    if (M <= 16) return launch_skinny_nt2<INT4, 1>(A, B, Sd, Z, C, M, N, K, g, st);
+    return launch_skinny_nt2<INT4, 2>(A, B, Sd, Z, C, M, N, K, g, st);
   }
   if (off32 && M <= 16)
-    return launch_skinny<INT4, 1, SK_PLAIN>(A, K, B, S, Z, nullptr, nullptr, nullptr, C, N, M, N,
+    return launch_skinny<INT4, 1, SK_PLAIN>(A, K, B, Sd, Z, nullptr, nullptr, nullptr, C, N, M, N,
                                             K, g, ws, ws_bytes, st);
   if (off32 && M <= 32)
-    return launch_skinny<INT4, 2, SK_PLAIN>(A, K, B, S, Z, nullptr, nullptr, nullptr, C, N, M, N,
+    return launch_skinny<INT4, 2, SK_PLAIN>(A, K, B, Sd, Z, nullptr, nullptr, nullptr, C, N, M, N,
                                             K, g, ws, ws_bytes, st);
   // The pipelined kernel stages scale rows in 8-column pieces (N % 8 == 0)
   // and whole 64-k chunks (K % 64 == 0).
@@ -1039,13 +1046,13 @@ int gemm_dispatch(const char* who, const f16* A, const uint32_t* B, const f16* S
     }
     switch (p.cfg) {
       case 0:
-        return launch_prefill2<INT4, SK_PLAIN, PF2_BIG>(A, K, B, S, Z, nullptr, nullptr, nullptr,
+        return launch_prefill2<U4, SK_PLAIN, PF2_BIG>(A, K, B, S, Z, nullptr, nullptr, nullptr,
                                                         C, N, M, N, K, g, p.ksplit, part, st);
       case 1:
-        return launch_prefill2<INT4, SK_PLAIN, PF2_MID>(A, K, B, S, Z, nullptr, nullptr, nullptr,
+        return launch_prefill2<U4, SK_PLAIN, PF2_MID>(A, K, B, S, Z, nullptr, nullptr, nullptr,
                                                         C, N, M, N, K, g, p.ksplit, part, st);
       default:
-        return launch_prefill2<INT4, SK_PLAIN, PF2_SMALL>(A, K, B, S, Z, nullptr, nullptr,
+        return launch_prefill2<U4, SK_PLAIN, PF2_SMALL>(A, K, B, S, Z, nullptr, nullptr,
                                                           nullptr, C, N, M, N, K, g, p.ksplit,
                                                           part, st);
     }
@@ -1053,9 +1060,9 @@ int gemm_dispatch(const char* who, const f16* A, const uint32_t* B, const f16* S
   // Prefill tiles: the largest tile that still gives about one block per CU.
   const long t256 = (long)mm_cdiv(M, 256) * mm_cdiv(N, 256);
   if (M > 128 && t256 >= 240)
-    return launch_prefill<INT4, 2, 2, 4>(A, K, B, S, Z, C, N, M, N, K, g, st);
-  if (M > 64) return launch_prefill<INT4, 2, 2, 2>(A, K, B, S, Z, C, N, M, N, K, g, st);
-  return launch_prefill<INT4, 1, 2, 2>(A, K, B, S, Z, C, N, M, N, K, g, st);
+    return launch_prefill<U4, 2, 2, 4>(A, K, B, S, Z, C, N, M, N, K, g, st);
+  if (M > 64) return launch_prefill<U4, 2, 2, 2>(A, K, B, S, Z, C, N, M, N, K, g, st);
+  return launch_prefill<U4, 1, 2, 2>(A, K, B, S, Z, C, N, M, N, K, g, st);
 }
 
 // Gate/up pair product (ACT = SK_SWIGLU or SK_PAIR) over two [K/8, N] packed
@@ -1382,8 +1389,17 @@ extern "C" int mm_fp4_gate_up_rowpacked(const uint16_t* A, const uint32_t* Bg, c
 extern "C" int mm_u4_gemm(const uint16_t* A, const uint32_t* B, const uint16_t* S,
                           const uint16_t* Z, uint16_t* C, int M, int N, int K, int g, void* ws,
                           size_t ws_bytes, void* stream) {
-  return gemm_dispatch<true>("mm_u4_gemm", (const f16*)A, B, (const f16*)S, (const f16*)Z,
+  return gemm_dispatch<1>("mm_u4_gemm", (const f16*)A, B, (const f16*)S, (const f16*)Z,
                              (f16*)C, M, N, K, g, ws, ws_bytes, (hipStream_t)stream);
+}
+
+extern "C" int mm_u4_gemm_sz(const uint16_t* A, const uint32_t* B, const uint16_t* S,
+                             const uint16_t* Z, const uint16_t* SZ, uint16_t* C, int M, int N,
+                             int K, int g, void* ws, size_t ws_bytes, void* stream) {
+  MM_CHECK_ARG(SZ != nullptr, "mm_u4_gemm_sz: SZ (interleaved scales and zeros) is required");
+  return gemm_dispatch<2>("mm_u4_gemm_sz", (const f16*)A, B, (const f16*)S, (const f16*)Z,
+                          (f16*)C, M, N, K, g, ws, ws_bytes, (hipStream_t)stream,
+                          (const f16*)SZ);
 }
 
 extern "C" int mm_fp4_gate_up(const uint16_t* A, const uint32_t* Bg, const uint16_t* Sg,

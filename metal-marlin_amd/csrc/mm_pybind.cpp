@@ -73,8 +73,11 @@ at::Tensor half_contig(const at::Tensor& t) {
 }
 
 // C = A . dequant(B, S[, Z]) for A [*, K], B [K/8, N] words; fp16 [*, N].
+// SZ (INT4 only, optional): the scales and zeros interleaved [K/g, N/4, 8]
+// for the decode kernels (mm_u4_gemm_sz).
 at::Tensor gemm(const at::Tensor& A, const at::Tensor& B, const at::Tensor& S,
-                const c10::optional<at::Tensor>& Z, int64_t group_size, int64_t stream) {
+                const c10::optional<at::Tensor>& Z, const c10::optional<at::Tensor>& SZ,
+                int64_t group_size, int64_t stream) {
   const int dev = A.get_device();
   if (dev < 0 || B.get_device() != dev || S.get_device() != dev ||
       (Z && Z->get_device() != dev)) {
@@ -110,6 +113,16 @@ at::Tensor gemm(const at::Tensor& A, const at::Tensor& B, const at::Tensor& S,
                      (const uint16_t*)s.data_ptr(), (uint16_t*)out.data_ptr(), (int)M, (int)N,
                      (int)K, (int)group_size, ws.data_ptr(), (size_t)ws.numel(),
                      (void*)stream);
+  } else if (SZ) {
+    const at::Tensor z = half_contig(*Z);
+    if (SZ->scalar_type() != at::kHalf || !SZ->is_contiguous() || SZ->numel() != 2 * z.numel() ||
+        SZ->get_device() != dev)
+      throw pybind11::value_error("SZ must be contiguous fp16 [K/g, 2N] on the operands' device");
+    rc = mm_u4_gemm_sz((const uint16_t*)a.data_ptr(), (const uint32_t*)b.data_ptr(),
+                       (const uint16_t*)s.data_ptr(), (const uint16_t*)z.data_ptr(),
+                       (const uint16_t*)SZ->data_ptr(), (uint16_t*)out.data_ptr(), (int)M,
+                       (int)N, (int)K, (int)group_size, ws.data_ptr(), (size_t)ws.numel(),
+                       (void*)stream);
   } else {
     const at::Tensor z = half_contig(*Z);
     rc = mm_u4_gemm((const uint16_t*)a.data_ptr(), (const uint32_t*)b.data_ptr(),
@@ -126,7 +139,7 @@ at::Tensor gemm(const at::Tensor& A, const at::Tensor& B, const at::Tensor& S,
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.doc() = "Per-call binding of libmmfp4's FP4 / INT4 GEMM entry points";
   m.def("gemm", &gemm, "C = A . dequant(B, S[, Z]) on the given stream", pybind11::arg("A"),
-        pybind11::arg("B"), pybind11::arg("S"), pybind11::arg("Z"),
+        pybind11::arg("B"), pybind11::arg("S"), pybind11::arg("Z"), pybind11::arg("SZ"),
         pybind11::arg("group_size"), pybind11::arg("stream"));
   m.def("workspace", &workspace_for,
         "the zero-initialised workspace of (device index, raw stream), at least nbytes",

@@ -101,6 +101,15 @@ MM_DEV f16x4 load_scales4(const f16* S, uint32_t gi, uint32_t col, int N, int G)
   }
 }
 
+// INT4 == 2: scales and zero points interleaved in one array SZ [K/g, N/4, 8]
+// (the 4 scales, then the 4 zero points, of each 4-column group): one 16-byte
+// load per lane and group instead of two 8-byte loads.
+MM_DEV void load_sz4(const f16* SZ, uint32_t gi, uint32_t col, int N, f16x4& s4, f16x4& z4) {
+  const f16x8 v = *at_bytes<f16x8>(SZ, (gi * (uint32_t)N + col) * 4u);
+  s4 = f16x4{v[0], v[1], v[2], v[3]};
+  z4 = f16x4{v[4], v[5], v[6], v[7]};
+}
+
 // One 64-column tile of a packed weight matrix: its packed words, scales and
 // (INT4) zeros, all [.., N] with row stride N, and the tile's first column.
 // Tiles of one wave may come from different matrices of the same shape.
@@ -140,7 +149,8 @@ struct SkTile {
 // four-column groups a lane reads stay contiguous, the lanes of a read pass
 // hit distinct bank groups, and the transposing stores of one instruction
 // hit 64 (DUAL: 32) distinct banks.
-template <bool INT4, int MT, int NT, int SPW, int FL, bool DUAL = false, bool SROW = false,
+// INT4: 0 FP4, 1 INT4 (zeros in tl.Z), 2 INT4 with SZ interleaved in tl.S.
+template <int INT4, int MT, int NT, int SPW, int FL, bool DUAL = false, bool SROW = false,
           bool ASTG = false, bool RT = false>
 MM_DEV void skinny_wave(const f16* __restrict__ A, int lda, const int* __restrict__ rowmap,
                         int rowdiv, int M, const SkTile (&tl)[NT], int N, int K, int g,
@@ -189,8 +199,12 @@ MM_DEV void skinny_wave(const f16* __restrict__ A, int lda, const int* __restric
         const uint32_t gi = (uint32_t)((stg * 32 * SLAB) / g);      // scalar
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-          s4[f][t] = load_scales4<SROW>(tl[t].S, gi, coff[t], N, K / g);
-          if constexpr (INT4) z4[f][t] = load_scales4<SROW>(tl[t].Z, gi, coff[t], N, K / g);
+          if constexpr (INT4 == 2) {
+            load_sz4(tl[t].S, gi, coff[t], N, s4[f][t], z4[f][t]);
+          } else {
+            s4[f][t] = load_scales4<SROW>(tl[t].S, gi, coff[t], N, K / g);
+            if constexpr (INT4) z4[f][t] = load_scales4<SROW>(tl[t].Z, gi, coff[t], N, K / g);
+          }
         }
       }
     }
@@ -308,14 +322,18 @@ MM_DEV void skinny_wave(const f16* __restrict__ A, int lda, const int* __restric
         const uint32_t gi = (uint32_t)((kp * 8) / g);
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-          const f16x4 s4 = load_scales4<SROW>(tl[t].S, gi, coff[t], N, K / g);
-          f16x4 z4 = {0, 0, 0, 0};
-          if constexpr (INT4) z4 = load_scales4<SROW>(tl[t].Z, gi, coff[t], N, K / g);
+          f16x4 s4, z4 = {0, 0, 0, 0};
+          if constexpr (INT4 == 2) {
+            load_sz4(tl[t].S, gi, coff[t], N, s4, z4);
+          } else {
+            s4 = load_scales4<SROW>(tl[t].S, gi, coff[t], N, K / g);
+            if constexpr (INT4) z4 = load_scales4<SROW>(tl[t].Z, gi, coff[t], N, K / g);
+          }
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             f16 nz = 0;
             if constexpr (INT4) nz = -clamp_zero(z4[j]);
-            const f16x8 b = WordDq<INT4>::run(w[i][t][j], sanitize_scale(s4[j]), nz);
+            const f16x8 b = WordDq<(INT4 != 0)>::run(w[i][t][j], sanitize_scale(s4[j]), nz);
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt)
               acc[mt][t][j] =
@@ -432,7 +450,7 @@ struct StripRound {
   f16x4 s[NF][NS], z[NF][NS];   // scale (and INT4 zero) rows of the round's groups
 };
 
-template <bool INT4, int NS, int SPW, int FL>
+template <int INT4, int NS, int SPW, int FL>
 MM_DEV void strip_wave(const f16* __restrict__ A, int lda, const int* __restrict__ rowmap,
                        int rowdiv, int M, const uint32_t* __restrict__ B,
                        const f16* __restrict__ S, const f16* __restrict__ Z, int N, int K, int g,
@@ -463,8 +481,12 @@ MM_DEV void strip_wave(const f16* __restrict__ A, int lda, const int* __restrict
       const uint32_t gi = (uint32_t)((slg * 32) / g);
 #pragma unroll
       for (int t = 0; t < NS; ++t) {
-        R.s[f][t] = *at_bytes<f16x4>(S, (gi * (uint32_t)N + scol[t]) * 2u);
-        if constexpr (INT4) R.z[f][t] = *at_bytes<f16x4>(Z, (gi * (uint32_t)N + scol[t]) * 2u);
+        if constexpr (INT4 == 2) {
+          load_sz4(S, gi, scol[t], N, R.s[f][t], R.z[f][t]);
+        } else {
+          R.s[f][t] = *at_bytes<f16x4>(S, (gi * (uint32_t)N + scol[t]) * 2u);
+          if constexpr (INT4) R.z[f][t] = *at_bytes<f16x4>(Z, (gi * (uint32_t)N + scol[t]) * 2u);
+        }
       }
     }
 #pragma unroll

@@ -40,6 +40,8 @@ SIGNATURES: dict[str, tuple] = {
                                           _c_int, _c_int, _vp, _c_size, _vp]),
     "mm_u4_gemm": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp,
                             _c_size, _vp]),
+    "mm_u4_gemm_sz": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int,
+                               _vp, _c_size, _vp]),
     "mm_fp4_gate_up": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int,
                                 _c_int, _vp, _c_size, _vp]),
     "mm_fp4_gemm_multi": (_c_int, [_vp, _c_int, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp,
@@ -136,13 +138,18 @@ def call(name: str, *args) -> None:
     check(getattr(F, name)(*args))
 
 
-def derived(src: torch.Tensor, key: str, build) -> torch.Tensor:
+def _stamp(t: torch.Tensor) -> tuple:
+    return (t._version, t.data_ptr(), tuple(t.shape), t.dtype)
+
+
+def derived(src: torch.Tensor, key: str, build, also: torch.Tensor | None = None):
     """build(src), cached on the tensor object `src` under `key` and rebuilt
-    when src is written in place (its version counter) or points at other
-    storage.  The copy lives exactly as long as the source tensor object; a
-    caller that passes a fresh view each time gets no caching."""
+    when src (or `also`, a second input of build) is written in place (its
+    version counter) or points at other storage.  The copy lives exactly as
+    long as the source tensor object; a caller that passes a fresh view each
+    time gets no caching."""
     cache = getattr(src, "_mmfp4_derived", None)
-    stamp = (src._version, src.data_ptr(), tuple(src.shape), src.dtype)
+    stamp = _stamp(src) + (_stamp(also) if also is not None else ())
     hit = cache.get(key) if cache is not None else None
     if hit is not None and hit[0] == stamp:
         return hit[1]

@@ -71,18 +71,37 @@ def _gemm(kind: str, A: torch.Tensor, B_packed: torch.Tensor, scales: torch.Tens
         sp = _lib.derived(scales, "pad4", lambda t: F.pad(t, pad, value=1.0))
         out = _gemm(kind, A, words, sp, zp, group_size)
         return out[..., :N].contiguous()
+    sz = None
+    if kind == "u4" and A.shape[-1] and A.numel() // A.shape[-1] <= 32 and _sz_ok(scales, zeros):
+        # decode sizes: scales and zero points interleaved once per (scales,
+        # zeros) pair, so the kernels load one 16-byte piece per group
+        sz = _lib.derived(scales, "sz", lambda t: _interleave_sz(t, zeros), also=zeros)
     fast = _BINDING if _BINDING is not None else _binding()
     if fast:
         # checks, output allocation and workspace in C++ (_mmfp4_torch.so)
         idx = A.get_device()
         try:
-            return fast.gemm(A, B_packed, scales, zeros if kind == "u4" else None, group_size,
+            return fast.gemm(A, B_packed, scales, zeros if kind == "u4" else None, sz, group_size,
                              _lib.raw_stream(idx) if idx >= 0 else 0)
         except RuntimeError as e:
             if type(e) is RuntimeError and "GPU only" not in str(e):
                 raise _lib.MMError(str(e)) from None
             raise
-    return _gemm_ctypes(kind, A, B_packed, scales, zeros, group_size)
+    return _gemm_ctypes(kind, A, B_packed, scales, zeros, group_size, sz)
+
+
+def _sz_ok(scales: torch.Tensor, zeros: torch.Tensor | None) -> bool:
+    return (zeros is not None and scales.dim() == 2 and zeros.shape == scales.shape
+            and scales.shape[-1] % 4 == 0 and scales.is_cuda and zeros.device == scales.device)
+
+
+def _interleave_sz(scales: torch.Tensor, zeros: torch.Tensor) -> torch.Tensor:
+    """[K/g, 2N] fp16: for each 4-column group its 4 scales then its 4 zero
+    points (the interleaved operand of mm_u4_gemm_sz)."""
+    R, N = scales.shape
+    s4 = scales.to(torch.float16).reshape(R, N // 4, 4)
+    z4 = zeros.to(torch.float16).reshape(R, N // 4, 4)
+    return torch.stack((s4, z4), dim=2).reshape(R, 2 * N).contiguous()
 
 
 _BINDING = None
@@ -95,7 +114,8 @@ def _binding():
 
 
 def _gemm_ctypes(kind: str, A: torch.Tensor, B_packed: torch.Tensor, scales: torch.Tensor,
-                 zeros: torch.Tensor | None, group_size: int) -> torch.Tensor:
+                 zeros: torch.Tensor | None, group_size: int,
+                 sz: torch.Tensor | None = None) -> torch.Tensor:
     # The per-call host path is kept short: one device check, the current
     # stream as a raw handle, a cached workspace, no copies of operands that
     # already have the right dtype and layout.
@@ -124,6 +144,11 @@ def _gemm_ctypes(kind: str, A: torch.Tensor, B_packed: torch.Tensor, scales: tor
     if kind == "fp4":
         rc = _lib.F.mm_fp4_gemm(a.data_ptr(), b.data_ptr(), s.data_ptr(), out.data_ptr(), M, N,
                                 K, group_size, ws.data_ptr(), ws.numel(), st)
+    elif sz is not None:
+        z = _half(zeros)
+        rc = _lib.F.mm_u4_gemm_sz(a.data_ptr(), b.data_ptr(), s.data_ptr(), z.data_ptr(),
+                                  sz.data_ptr(), out.data_ptr(), M, N, K, group_size,
+                                  ws.data_ptr(), ws.numel(), st)
     else:
         z = _half(zeros)
         rc = _lib.F.mm_u4_gemm(a.data_ptr(), b.data_ptr(), s.data_ptr(), z.data_ptr(),

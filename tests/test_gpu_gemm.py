@@ -350,3 +350,36 @@ def test_workspace_shared_between_call_paths_and_released():
     torch.cuda.synchronize()
     w2 = _lib.workspace_on(dev.index, st, 4096)
     assert int(w2[:65536].count_nonzero()) == 0       # fresh, zeroed counters
+
+
+@pytest.mark.parametrize("M,K,N,g", [(1, 4096, 6144, 128), (4, 4096, 4096, 64), (12, 4096, 4096, 128),
+                                     (16, 4096, 28672, 128), (1, 14336, 4096, 128),
+                                     (24, 2048, 3072, 32), (32, 4096, 1024, 256), (9, 1024, 2048, 8)])
+def test_u4_interleaved_scales_zeros_bit_identical(rng, M, K, N, g):
+    """mm_u4_gemm_sz (scales and zero points interleaved for the decode
+    kernels) gives mm_u4_gemm's bits on every decode kernel family (two-slab,
+    strip, 64- and 128-column skinny, split-K, pre-scale g=8), through the C
+    ABI; marlin_gemm_int4 caches the interleaved copy on the scales tensor and
+    rebuilds it when the zeros change."""
+    import mmfp4
+    from mmfp4 import _lib, kernels
+    q, s, z = ofp4.pack_u4_weights(rng.normal(0, 0.02, (N, K)).astype(np.float16), g)
+    a = to_dev(rng.normal(0, 1, (M, K)).astype(np.float16))
+    dq, ds, dz = to_dev(q), to_dev(s), to_dev(z)
+    sz = kernels._interleave_sz(ds, dz)
+    ws = _lib.workspace(a.device, int(_lib.load().mm_gemm_workspace_bytes(M, N, K)))
+    outs = []
+    for name, extra in (("mm_u4_gemm", ()), ("mm_u4_gemm_sz", (_lib.ptr(sz),))):
+        out = torch.empty((M, N), dtype=torch.float16, device=a.device)
+        announce(f"{name} M={M} K={K} N={N} g={g}")
+        _lib.call(name, _lib.ptr(a), _lib.ptr(dq), _lib.ptr(ds), _lib.ptr(dz), *extra,
+                  _lib.ptr(out), M, N, K, g, _lib.ptr(ws), ws.numel(), _lib.stream_of(a))
+        outs.append(out)
+    assert torch.equal(outs[0], outs[1])
+    assert torch.equal(mmfp4.marlin_gemm_int4(a, dq, ds, dz, g), outs[0])
+    cached = ds._mmfp4_derived["sz"][1]
+    dz.add_(1)                                   # new zero points: the copy is rebuilt
+    out2 = mmfp4.marlin_gemm_int4(a, dq, ds, dz, g)
+    assert ds._mmfp4_derived["sz"][1] is not cached
+    ref = ofp4.gemm_u4_ref(to_np(a), q, s, z + 1, g)
+    assert max_abs_rel(to_np(out2), ref) <= TOL
