@@ -683,7 +683,9 @@ k_splitk_reduce(const float* __restrict__ part, int ks, int M, int N, f16* __res
 #define MM_SK_NW2 8         // waves per skinny block, 16 < M <= 32
 #define MM_SK_SPW1 8        // 32-k steps per wave per round, M <= 16
 #define MM_SK_SPW2 4        // 32-k steps per wave per round, 16 < M <= 32
-#define MM_SK_KS2 4         // max K split for 16 < M <= 32 (bounds partial traffic)
+#define MM_SK_KS2 8         // max K split for 16 < M <= 32 (bounds partial traffic;
+                            // 4 -> 8 measured on MI355X: 14336x4096 at M=17/24/32
+                            // 13.9/14.5/15.0 -> 13.2/14.1/14.8 us, others unchanged)
 #define MM_SK_NOSPLIT_TILES 200   // column tiles from which the K range is not split
 #define MM_SK_NOSPLIT_TILES1 96   // the same for M <= 16
 #define MM_SK_MAXBLOCKS 2048
@@ -802,11 +804,14 @@ int launch_skinny(const f16* A, int lda, const uint32_t* B, const f16* S, const 
 
 // Plain skinny product with two 64-column tiles per block and the whole K
 // range per block (no split, so no workspace is touched).  The caller
-// guarantees at least MM_SK_NOSPLIT_TILES blocks.
-template <int INT4, int MT>
+// guarantees at least MM_SK_NOSPLIT_TILES blocks.  NW: waves per block; the
+// dispatcher takes 4 from 24 rows up (measured on MI355X, 4096 x 28672:
+// M=32 21.3 -> 19.8 us, M=24 20.3 -> 19.6 us with 4 waves; M=17 18.6 ->
+// 19.9 us, so 8 below).
+template <int INT4, int MT, int NW = sk_nw<MT>()>
 int launch_skinny_nt2(const f16* A, const uint32_t* B, const f16* S, const f16* Z, f16* C, int M,
                       int N, int K, int g, hipStream_t st) {
-  constexpr int NT = 2, SPW = sk_spw<MT>(), NW = sk_nw<MT>();
+  constexpr int NT = 2, SPW = sk_spw<MT>();
   const int nrounds = mm_cdiv((K / 8 + 3) / 4, NW * SPW);
   const dim3 grid(mm_cdiv(N, NT * SK_COLS), 1);
   const SkMulti none{};
@@ -1024,6 +1029,7 @@ int gemm_dispatch(const char* who, const f16* A, const uint32_t* B, const f16* S
   // 24.6 -> 20.4 us; at M <= 8 and on narrower layers the 64-column plan wins).
   if (off32 && M > 8 && M <= 32 && mm_cdiv(N, 2 * SK_COLS) >= MM_SK_NOSPLIT_TILES) {
     if (M <= 16) return launch_skinny_nt2<INT4, 1>(A, B, Sd, Z, C, M, N, K, g, st);
+    if (M >= 24) return launch_skinny_nt2<INT4, 2, 4>(A, B, Sd, Z, C, M, N, K, g, st);
     return launch_skinny_nt2<INT4, 2>(A, B, Sd, Z, C, M, N, K, g, st);
   }
   if (off32 && M <= 16)
