@@ -129,29 +129,92 @@ def run_layer_bench(torch, mmfp4, M: int, steps: int, warmup: int, int4: bool = 
             "per_shape": per_shape, "copies": copies}
 
 
+# Read-kernel configurations (blocks, threads, 16-byte loads in flight per
+# lane, mode: bit 0 non-temporal, bit 1 grid-stride order) that came out on
+# top of a 336-point sweep of mm_stream_read on MI355X for 8.7-60.6 MB
+# (profiles/hbm_read_ceiling_sweep.md); the first is the aid's default plan.
+READ_CONFIGS = [(0, 0, 4, 1), (4096, 512, 2, 3), (1024, 512, 4, 1), (2048, 1024, 2, 1),
+                (1024, 512, 2, 3), (2048, 512, 2, 3), (8192, 256, 2, 3), (4096, 512, 2, 1)]
+
+
+def best_read(torch, nbytes: int, steps: int, warmup: int):
+    """The fastest of READ_CONFIGS for one read of `nbytes` (rotated buffers
+    past the Infinity Cache, back-to-back launches, HIP events): (µs, config,
+    launch builder for that config)."""
+    import bench_aids
+    copies = max(2, -(-ROTATE_BYTES // nbytes))
+    bufs = [torch.empty(nbytes, dtype=torch.uint8, device="cuda") for _ in range(copies)]
+    sink = torch.empty(16384 * 1024, dtype=torch.int32, device="cuda")
+    st = torch.cuda.current_stream().cuda_stream
+
+    def mk(cfg):
+        return [[lambda b=b: bench_aids.call("mm_stream_read", b.data_ptr(), nbytes,
+                                             sink.data_ptr(), sink.numel() * 4, *cfg, st)]
+                for b in bufs]
+    best = None
+    for cfg in READ_CONFIGS:
+        us = 1e3 * timed_launches(torch, mk(cfg), steps, warmup) / steps
+        if best is None or us < best[0]:
+            best = (us, cfg)
+    return best[0], best[1], mk
+
+
+def run_read_sweep(torch):
+    """Sweep mm_stream_read over grid, loads in flight, cache hint and order
+    for the layer's read sizes (8.7, 13.0, 30.3 and 60.6 MB): µs per launch,
+    back to back over rotated buffers, best of three timed batches of 60."""
+    import itertools
+    import bench_aids
+    st = torch.cuda.current_stream().cuda_stream
+    sink = torch.empty(16384 * 1024, dtype=torch.int32, device="cuda")
+    rows = []
+    for nbytes in (8_650_752, 12_999_984, 30_277_632, 60_555_264):
+        copies = max(2, -(-800_000_000 // nbytes))
+        bufs = [torch.empty(nbytes, dtype=torch.uint8, device="cuda") for _ in range(copies)]
+        for blocks, threads, unroll, mode in itertools.product(
+                (256, 512, 1024, 2048, 4096, 8192, 16384), (256, 512, 1024), (2, 4, 8, 16),
+                (0, 1, 2, 3)):
+            if blocks * threads > 16384 * 1024:
+                continue
+            cfg = (blocks, threads, unroll, mode)
+            launches = [[lambda b=b, cfg=cfg: bench_aids.call(
+                "mm_stream_read", b.data_ptr(), nbytes, sink.data_ptr(), sink.numel() * 4, *cfg,
+                st)] for b in bufs]
+            us = min(1e3 * timed_launches(torch, launches, 60, 4) / 60 for _ in range(3))
+            rows.append({"bytes": nbytes, "blocks": blocks, "threads": threads,
+                         "unroll": unroll, "mode": mode, "us": round(us, 3),
+                         "TBps": round(nbytes / us / 1e6, 3)})
+        del bufs
+        torch.cuda.empty_cache()
+    best = {}
+    for r in rows:
+        if r["bytes"] not in best or r["us"] < best[r["bytes"]]["us"]:
+            best[r["bytes"]] = r
+    return {"best": list(best.values()), "points": len(rows), "all": rows}
+
+
 def run_read_ceiling(torch, steps: int, warmup: int):
     """The HBM read rate this GPU reaches for the same bytes in the same
     back-to-back launch pattern: `mm_stream_read` (a read-only stream, no
-    decode, no math) over each layer GEMM's packed weights + scales, rotated
-    copies, timed exactly like the GEMMs.  The practical ceiling of a
-    weight-streaming kernel of that size (launch, ramp-up and drain included)."""
-    import bench_aids
-    sizes = [(name, -(-alg_bytes(0, K, N) // 16) * 16) for name, K, N in LLAMA_LAYER]
-    copies = max(2, -(-ROTATE_BYTES // sum(b for _, b in sizes)))
-    bufs = [[torch.empty(b, dtype=torch.uint8, device="cuda") for _, b in sizes]
-            for _ in range(copies)]
-    sink = torch.empty(8192 * 512, dtype=torch.int32, device="cuda")
-    st = torch.cuda.current_stream().cuda_stream
-
-    def rd(buf):
-        return lambda: bench_aids.call("mm_stream_read", buf.data_ptr(), buf.numel(),
-                                       sink.data_ptr(), sink.numel() * 4, 0, 0, 4, 1, st)
-    launches = [[rd(b) for b in row] for row in bufs]
-    total_ms = timed_launches(torch, launches, steps, warmup)
-    per = {name: round(us, 3) for (name, _), us in zip(sizes, per_shape_us(torch, launches))}
-    byts = sum(b for _, b in sizes)
-    return {"kernel": "mm_stream_read (16-byte non-temporal loads, no writes)",
-            "per_shape_us": per, "layer_us": round(1e3 * total_ms / steps, 3),
+    decode, no math, nothing written; bench_aids) over each layer GEMM's
+    packed weights + scales, rotated copies, timed exactly like the GEMMs, in
+    the best of READ_CONFIGS for each size.  The practical ceiling of a
+    weight-streaming kernel of that size (launch, ramp-up and drain
+    included)."""
+    per, cfgs, launches = {}, {}, []
+    for name, K, N in LLAMA_LAYER:
+        nbytes = -(-alg_bytes(0, K, N) // 16) * 16
+        us, cfg, mk = best_read(torch, nbytes, steps, warmup)
+        per[name], cfgs[name] = round(us, 3), list(cfg)
+        launches.append(mk(cfg))
+    n = min(len(x) for x in launches)
+    step = [[launches[j][i][0] for j in range(len(LLAMA_LAYER))] for i in range(n)]
+    total_ms = timed_launches(torch, step, steps, warmup)
+    byts = sum(-(-alg_bytes(0, K, N) // 16) * 16 for _, K, N in LLAMA_LAYER)
+    return {"kernel": "mm_stream_read (bench_aids: 16-byte loads, no writes), best of "
+                      f"{len(READ_CONFIGS)} configurations per size",
+            "per_shape_us": per, "per_shape_config": cfgs,
+            "layer_us": round(1e3 * total_ms / steps, 3),
             "layer_TBps": round(byts / (total_ms / steps * 1e-3) / 1e12, 3)}
 
 
@@ -234,7 +297,9 @@ def rand_weights(torch, K: int, N: int, gen):
 def run_north_star_decode(torch, mmfp4, steps: int):
     """The north star's decode shapes at M=1 (4096 -> 14336 and 14336 -> 4096),
     each on its own with rotated weight copies: µs per launch, algorithmic
-    TB/s, fraction of HBM peak and of the 0.70 target."""
+    TB/s, fraction of HBM peak and of the 0.70 target, and beside it the best
+    single-launch read of the same weight bytes (best_read) and the GEMM's
+    fraction of that read time."""
     out = {}
     for name, K, N in (("4096x14336", 4096, 14336), ("14336x4096", 14336, 4096)):
         copies = max(2, -(-ROTATE_BYTES // alg_bytes(0, K, N)))
@@ -243,10 +308,15 @@ def run_north_star_decode(torch, mmfp4, steps: int):
         launches = [[lambda w=w: mmfp4.marlin_gemm_fp4(a, w[0], w[1], G)] for w in ws]
         us = 1e3 * timed_launches(torch, launches, steps, 10) / steps
         tbs = alg_bytes(1, K, N) / (us * 1e-6) / 1e12
+        del ws
+        ceil_us, cfg, _ = best_read(torch, -(-alg_bytes(0, K, N) // 16) * 16, steps, 10)
         out[name] = {"us": round(us, 3), "TBps": round(tbs, 3),
                      "frac_hbm_peak": round(tbs * 1e3 / HBM_PEAK_GBS, 4),
-                     "frac_of_0.70_target": round(tbs * 1e3 / HBM_PEAK_GBS / 0.70, 4)}
-        del ws
+                     "frac_of_0.70_target": round(tbs * 1e3 / HBM_PEAK_GBS / 0.70, 4),
+                     "read_ceiling_us": round(ceil_us, 3), "read_ceiling_config": list(cfg),
+                     "read_ceiling_frac_hbm_peak": round(
+                         alg_bytes(0, K, N) / (ceil_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                     "frac_of_read_ceiling": round(ceil_us / us, 4)}
     return out
 
 
@@ -596,7 +666,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--all", action="store_true", help="accepted for compatibility; every "
                     "BASELINE config is reported by default")
-    ap.add_argument("--section", choices=("all", "layer", "prefill", "moe", "fused", "graph"),
+    ap.add_argument("--section", choices=("all", "layer", "prefill", "moe", "fused", "graph",
+                                          "read_sweep"),
                     default="all",
                     help="run one workload alone (for profiling); the default runs all and "
                          "prints the contract line")
@@ -630,6 +701,8 @@ def main() -> int:
             tf = r["flops"] / (r["ms_per_step"] * 1e-3) / 1e12
             res = {"ms_per_step": round(r["ms_per_step"], 4), "per_shape": r["per_shape"],
                    "TFLOPs": round(tf, 1), "mfma_ceiling": run_mfma_ceiling(torch, mmfp4, tf)}
+        elif args.section == "read_sweep":
+            res = run_read_sweep(torch)
         elif args.section == "graph":
             res = run_layer_graph(torch, mmfp4, 200)
         elif args.section == "moe":
