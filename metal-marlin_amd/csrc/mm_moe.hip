@@ -57,6 +57,11 @@ constexpr int SORT_KC = 8;          // 64-key chunks fetched together per wave
 // 121 / 126 us, 8192 171 / 178 us, 16384 292 / 288 us, 32768 474 / 460 us.
 #define MM_MOE_SORT_ONE_BLOCK 8192
 #define MM_MOE_SORT_SEG 1024
+// The single-launch multi-block sort (k_moe_sort_mb) serves MB_MIN < n <= MB_MAX
+// assignments with E <= MB_EXPERTS (its LDS holds (2 + 16) * E counters).
+#define MM_MOE_SORT_MB_MIN 2048
+#define MM_MOE_SORT_MB_MAX 32768
+#define MM_MOE_SORT_MB_EXPERTS 512
 
 // Stable counting sort in one block.  Wave w owns the w-th contiguous
 // segment of the flat assignments (whole 64-element chunks), so segment order
@@ -252,6 +257,138 @@ k_moe_sort(const IdT* __restrict__ ids, int n, int E, int kin, int32_t* __restri
       if (e >= 0 && (same & below) == 0) mine[e] += __popcll(same);
       place_dropped(e, i);
     }
+  }
+}
+
+// Stable counting sort over several blocks in ONE launch, with no
+// communication between blocks: block b owns the b-th SORT_THREADS-long
+// segment of the flat assignments (one per thread) and first counts, in LDS
+// with integer atomics, every expert's assignments over ALL n ids and over the
+// ids before its segment (all blocks read all ids, from L2).  From those it
+// knows each expert's offset and where its own segment's rows of that expert
+// start, and places its segment with the in-wave ranks of the one-block sort
+// (ballot matching) and per-wave counts.  The result is the one-block sort's
+// (same order, same dropped-id handling); block 0 writes the offsets.  The
+// per-block cost grows with n (every block counts all ids), so the host uses
+// it for mid-sized inputs only.  Dynamic LDS: (2 + SORT_WAVES) * E ints.
+template <typename IdT, bool SH>
+__global__ void __launch_bounds__(SORT_THREADS)
+k_moe_sort_mb(const IdT* __restrict__ ids, int n, int E, int kin, int32_t* __restrict__ offsets,
+              int32_t* __restrict__ sorted_idx, int32_t* __restrict__ inverse) {
+  extern __shared__ int sm[];
+  int* const tot = sm;              // [E] assignments per expert, all ids
+  int* const pre = sm + E;          // [E] the same over ids before this segment
+  int* const wpos = sm + 2 * E;     // [SORT_WAVES][E] per-wave counts -> start positions
+  __shared__ int wsum[SORT_WAVES];
+  __shared__ int winv[SORT_WAVES];  // dropped ids per wave of this segment
+  __shared__ int s_drop;            // dropped ids before this segment
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nbits = E > 1 ? 32 - __clz(E - 1) : 0;
+  const int seg0 = blockIdx.x * SORT_THREADS;
+  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  for (int x = tid; x < (2 + SORT_WAVES) * E; x += SORT_THREADS) sm[x] = 0;
+  if (tid == 0) s_drop = 0;
+  __syncthreads();
+
+  // Key of flat assignment i: its expert, -1 for an id outside the range
+  // (dropped), -2 past the end.
+  auto key_at = [&](int i) {
+    if constexpr (SH) {
+      const int t = i / (kin + 1), j = i - t * (kin + 1);
+      if (i >= n) return -2;
+      if (j == kin) return E - 1;
+      const long long v = (long long)ids[min(t * kin + j, n / (kin + 1) * kin - 1)];
+      return (v >= 0 && v < E - 1) ? (int)v : -1;
+    } else {
+      const long long v = (long long)ids[min(i, n - 1)];
+      return i >= n ? -2 : ((v >= 0 && v < E) ? (int)v : -1);
+    }
+  };
+
+  // Pass A: histograms of all ids and of the ids before the segment.  The
+  // keys of SORT_KC rounds are loaded together so their loads overlap.
+  int dpre = 0;
+  for (int i0 = 0; i0 < n; i0 += SORT_THREADS * SORT_KC) {
+    int key[SORT_KC];
+#pragma unroll
+    for (int u = 0; u < SORT_KC; ++u) key[u] = key_at(i0 + u * SORT_THREADS + tid);
+#pragma unroll
+    for (int u = 0; u < SORT_KC; ++u) {
+      const int i = i0 + u * SORT_THREADS + tid;
+      const int e = key[u];
+      if (e >= 0) {
+        __hip_atomic_fetch_add(&tot[e], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        if (i < seg0)
+          __hip_atomic_fetch_add(&pre[e], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      } else if (e == -1) {
+        dpre += i < seg0;
+      }
+    }
+  }
+  // Own assignment: rank among the equal keys of lower lanes in the wave, and
+  // the wave's count per expert (by the group's leader lane).
+  const int i = seg0 + tid;
+  const int e = key_at(i);
+  uint64_t same = 0;
+  {
+    const bool valid = e >= 0;
+    uint64_t m = __ballot(valid);
+    for (int bit = 0; bit < nbits; ++bit) {
+      const bool on = valid && ((e >> bit) & 1);
+      const uint64_t bb = __ballot(on);
+      m &= on ? bb : ~bb;
+    }
+    same = valid ? m : 0ull;
+  }
+  const int rank = __popcll(same & below);
+  if (e >= 0 && rank == 0) wpos[wave * E + e] = __popcll(same);
+  const uint64_t dm = __ballot(e == -1);
+  if (lane == 0) winv[wave] = __popcll(dm);
+  // dropped ids before the segment: one LDS add per wave
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) dpre += __shfl_xor(dpre, d);
+  if (lane == 0)
+    __hip_atomic_fetch_add(&s_drop, dpre, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  __syncthreads();
+
+  // Exclusive offsets over experts (wave scans, then the wave sums), then each
+  // wave's first position per expert: offset + ids of the expert before the
+  // segment + those of the earlier waves of the segment.
+  const int c = tid < E ? tot[tid] : 0;
+  int incl = c;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int o = __shfl_up(incl, d);
+    if (lane >= d) incl += o;
+  }
+  if (lane == 63) wsum[wave] = incl;
+  __syncthreads();
+  int wbase = 0;
+  for (int w = 0; w < wave; ++w) wbase += wsum[w];
+  int nvalid = 0;
+  for (int w = 0; w < SORT_WAVES; ++w) nvalid += wsum[w];
+  if (tid < E) {
+    const int off = wbase + incl - c;
+    if (blockIdx.x == 0) offsets[tid] = off;
+    int run = off + pre[tid];
+    for (int w = 0; w < SORT_WAVES; ++w) {
+      const int cw = wpos[w * E + tid];
+      wpos[w * E + tid] = run;
+      run += cw;
+    }
+  }
+  if (blockIdx.x == 0 && tid == 0) offsets[E] = nvalid;
+  __syncthreads();
+  if (e >= 0) {
+    const int pos = wpos[wave * E + e] + rank;
+    sorted_idx[pos] = i;
+    inverse[i] = pos;
+  } else if (e == -1) {
+    int tail = nvalid + s_drop;
+    for (int w = 0; w < wave; ++w) tail += winv[w];
+    const int pos = tail + __popcll(dm & below);
+    sorted_idx[pos] = i;
+    inverse[i] = pos;
   }
 }
 
@@ -516,7 +653,17 @@ int moe_sort(const char* who, const IdT* expert_ids, int T, int k, int E, int32_
   const size_t lds = (size_t)SORT_WAVES * E * sizeof(int);
   const int n = T * kt;
   hipStream_t st = (hipStream_t)stream;
-  if (cnt != nullptr && n > MM_MOE_SORT_ONE_BLOCK) {
+  if (n > MM_MOE_SORT_MB_MIN && n <= MM_MOE_SORT_MB_MAX && E <= MM_MOE_SORT_MB_EXPERTS) {
+    // Mid-sized inputs: several blocks in one launch, each counting every id.
+    const int nb = mm_cdiv(n, SORT_THREADS);
+    const size_t lds_mb = (size_t)(2 + SORT_WAVES) * E * sizeof(int);
+    if (shared)
+      hipLaunchKernelGGL((k_moe_sort_mb<IdT, true>), dim3(nb), dim3(SORT_THREADS), lds_mb, st,
+                         expert_ids, n, E, k, offsets, sorted_idx, inverse);
+    else
+      hipLaunchKernelGGL((k_moe_sort_mb<IdT, false>), dim3(nb), dim3(SORT_THREADS), lds_mb, st,
+                         expert_ids, n, E, k, offsets, sorted_idx, inverse);
+  } else if (cnt != nullptr && n > MM_MOE_SORT_ONE_BLOCK) {
     // Blocks of MM_MOE_SORT_SEG assignments: a count launch, then a place
     // launch (cnt: nb * (E + 1) ints of caller scratch).
     const int nb = mm_cdiv(n, MM_MOE_SORT_SEG);
