@@ -58,8 +58,13 @@ constexpr int SORT_KC = 8;          // 64-key chunks fetched together per wave
 #define MM_MOE_SORT_ONE_BLOCK 8192
 #define MM_MOE_SORT_SEG 1024
 // The single-launch multi-block sort (k_moe_sort_mb) serves MB_MIN < n <= MB_MAX
-// assignments with E <= MB_EXPERTS (its LDS holds (2 + 16) * E counters).
-#define MM_MOE_SORT_MB_MIN 2048
+// assignments with E <= MB_EXPERTS (its LDS holds (2 + 16) * E counters);
+// n > 0 always (an empty input takes the one-block kernel).  Measured on
+// MI355X, whole Qwen3-30B-A3B MLP call against the one-block sort: T = 8 / 32
+// / 128 / 256 / 1024 / 2048 43.1 -> 41.2, 66.3 -> 64.5, 78.4 -> 75.3, 117.0
+// -> 113.5, 155.4 -> 151.1, 269.3 -> 253.8 us (sort alone at T = 1024:
+// 14-17 -> 7.3 us).
+#define MM_MOE_SORT_MB_MIN 0
 #define MM_MOE_SORT_MB_MAX 32768
 #define MM_MOE_SORT_MB_EXPERTS 512
 
