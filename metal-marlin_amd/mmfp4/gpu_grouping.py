@@ -1,5 +1,5 @@
 """Expert grouping manager API (the reference's `metal_marlin.moe.gpu_grouping`
-surface), backed by the device counting sort `k_moe_sort` in libmmfp4.so.
+surface), backed by the device counting sort of libmmfp4.so (`mm_moe_sort`).
 
 Reference: metal_marlin/moe/gpu_grouping.py:30-75 (GPUGroupingResult),
 :96-152 (group_tokens_by_expert_gpu_optimized), :155-221
