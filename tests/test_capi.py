@@ -102,3 +102,34 @@ def test_new_entry_points_validate():
         _lib.call("mm_moe_mlp_shared_fp4", None, None, 0, None, 4, 2, 8, 256, 128, None, None,
                   None, None, None, None, None, None, ctypes.c_float(1.0), None, 128, None, None,
                   None, None, None)
+
+
+def test_measurement_aids_live_outside_the_gemm_abi():
+    """bench.py's read-ceiling and MFMA-ceiling probes are exported by the
+    bench-only library, not by libmmfp4.so; their argument checks run without
+    a GPU."""
+    import bench_aids
+    lib = _lib.load()
+    for name in ("mm_stream_read", "mm_mfma_ceiling"):
+        assert not hasattr(lib, name), name
+        assert hasattr(bench_aids.load(), name), name
+    with pytest.raises(ValueError, match="unroll"):
+        bench_aids.call("mm_stream_read", ctypes.c_void_p(256), 4096, ctypes.c_void_p(256),
+                        1 << 20, 64, 64, 3, 1, None)
+    with pytest.raises(ValueError, match="n_halves"):
+        bench_aids.call("mm_mfma_ceiling", ctypes.c_void_p(256), ctypes.c_void_p(256), 12, 1,
+                        ctypes.c_void_p(256), 1 << 20, None)
+
+
+def test_calibrated_quantizer_and_interleaved_int4_validate():
+    with pytest.raises(ValueError, match="order statistics"):
+        _lib.call("mm_fp4_quantize_calibrated", None, 1, 4, 256, 128, 1, 130, 131,
+                  ctypes.c_float(0.5), 0, ctypes.c_float(0.0), ctypes.c_float(1.0),
+                  ctypes.c_double(1.0), ctypes.c_double(1.0), None, None, None)
+    with pytest.raises(ValueError, match="mode"):
+        _lib.call("mm_fp4_quantize_calibrated", None, 1, 4, 256, 128, 0, 0, 0,
+                  ctypes.c_float(0.0), 3, ctypes.c_float(0.0), ctypes.c_float(1.0),
+                  ctypes.c_double(1.0), ctypes.c_double(1.0), None, None, None)
+    with pytest.raises(ValueError, match="SZ"):
+        _lib.call("mm_u4_gemm_sz", None, None, None, None, None, None, 1, 64, 64, 32, None, 0,
+                  None)
