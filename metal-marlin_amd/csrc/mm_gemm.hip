@@ -96,7 +96,7 @@ k_skinny(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
   // 69.7 -> 66.4 us; two-tile blocks, e.g. 4096 x 28672 at M=32, were slower
   // with it, 21.0 -> 22.0 us).
   constexpr bool ASTG = !STAGE && NT == 1 && 16 * MT * 4 * SPW == 512;
-  constexpr int RED = (NW > 1 ? NW - 1 : 1) * MT * NT * 16 * 64;
+  constexpr int RED = row_items_lds_floats<MT, NT, NW>();
   constexpr int STG = STAGE ? NW * NT * 2048 : (ASTG ? NW * 2048 : 0);
   constexpr int LDSF = STG > RED ? STG : RED;   // floats
   __shared__ __attribute__((aligned(16))) float red[LDSF];
@@ -155,66 +155,61 @@ k_skinny(const f16* __restrict__ A, int lda, const uint32_t* __restrict__ B,
                                                          blk_st0 + wave * SPW, nrounds, NW * SPW,
                                                          acc);
   }
-  skinny_block_reduce<MT, NT, NW>(red, acc, M);
+  // Row items (mt, rr): lane (c, q) of the owning wave holds row
+  // 16*mt + 4*q + rr, columns 4*c .. 4*c + 3 of each tile.
+  constexpr int IPW = row_items_per_wave<MT, NW>();
+  f32x4 rv[IPW][NT];
+  block_reduce_items<MT, NT, NW>(red, acc, M, rv);
+  auto item_row = [&](int k) {
+    const int it = wave + k * NW;
+    return it < MT * 4 ? 16 * (it >> 2) + 4 * q + (it & 3) : M;
+  };
 
-  // Lane (c, q) of wave 0 holds rows 16*mt + 4*q + rr, columns 4*c + j of
-  // each tile.
   if (ksplit == 1) {
-    if (wave != 0) return;
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+    for (int k = 0; k < IPW; ++k) {
+      const int row = item_row(k);
+      if (row >= M) continue;
+      if constexpr (ACT == SK_SWIGLU) {
+        const int col = n0 + 4 * c;
+        if (col < N)
+          *(f16x4*)(C + (size_t)row * ldc + col) =
+              f16x4{(f16)swiglu(rv[k][0][0], rv[k][1][0]), (f16)swiglu(rv[k][0][1], rv[k][1][1]),
+                    (f16)swiglu(rv[k][0][2], rv[k][1][2]), (f16)swiglu(rv[k][0][3], rv[k][1][3])};
+      } else {
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const int row = mt * 16 + 4 * q + rr;
-        if (row >= M) continue;
-        if constexpr (ACT == SK_SWIGLU) {
-          const int col = n0 + 4 * c;
+        for (int t = 0; t < NT; ++t) {
+          const int col = ONE ? n0 + t * SK_COLS + 4 * c : n0 + 4 * c;
           if (col < N)
-            *(f16x4*)(C + (size_t)row * ldc + col) =
-                f16x4{(f16)swiglu(acc[mt][0][0][rr], acc[mt][1][0][rr]),
-                      (f16)swiglu(acc[mt][0][1][rr], acc[mt][1][1][rr]),
-                      (f16)swiglu(acc[mt][0][2][rr], acc[mt][1][2][rr]),
-                      (f16)swiglu(acc[mt][0][3][rr], acc[mt][1][3][rr])};
-        } else {
-#pragma unroll
-          for (int t = 0; t < NT; ++t) {
-            const int col = ONE ? n0 + t * SK_COLS + 4 * c : n0 + 4 * c;
-            if (col < N)
-              *(f16x4*)(C + (size_t)row * ldc + ccol(t)) =
-                  f16x4{(f16)acc[mt][t][0][rr], (f16)acc[mt][t][1][rr], (f16)acc[mt][t][2][rr],
-                        (f16)acc[mt][t][3][rr]};
-          }
+            *(f16x4*)(C + (size_t)row * ldc + ccol(t)) =
+                f16x4{(f16)rv[k][t][0], (f16)rv[k][t][1], (f16)rv[k][t][2], (f16)rv[k][t][3]};
         }
       }
+    }
     return;
   }
   // K split across blocks: publish this block's partial tile, then the last
   // block of the column tile sums all partials in split order.  Partials are
   // moved with 16-byte sc1 buffer accesses (the agent-scope policy: coherent
   // across the XCDs' L2s without writing back whole caches) and the counter
-  // with an agent-scope atomic; waiting for this wave's stores orders them
+  // with an agent-scope atomic; waiting for each wave's stores orders them
   // before the counter bump.
   const __amdgpu_buffer_rsrc_t prs = mm_rsrc(part);
-  if (wave == 0) {
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+  for (int k = 0; k < IPW; ++k) {
+    const int row = item_row(k);
+    if (row >= M) continue;
 #pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        const int col = ONE ? n0 + t * SK_COLS + 4 * c : n0 + 4 * c;
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          const int row = mt * 16 + 4 * q + rr;
-          if (row < M && col < N)
-            store_agent_x4(prs, 4u * (uint32_t)((blockIdx.y * M + row) * PW + pcol(t)),
-                           f32x4{acc[mt][t][0][rr], acc[mt][t][1][rr], acc[mt][t][2][rr],
-                                 acc[mt][t][3][rr]});
-        }
-      }
+    for (int t = 0; t < NT; ++t) {
+      const int col = ONE ? n0 + t * SK_COLS + 4 * c : n0 + 4 * c;
+      if (col < N)
+        store_agent_x4(prs, 4u * (uint32_t)((blockIdx.y * M + row) * PW + pcol(t)), rv[k][t]);
+    }
   }
   // Hand-off.  The partials are sc1 stores (coherent across the XCDs' L2s);
-  // s_waitcnt(0) waits until they are performed at that coherence point
-  // before thread 0 (of the same wave 0) bumps the arrival counter, and the
-  // last block reads them with sc1 loads.
+  // each wave's s_waitcnt(0) waits until its stores are performed at that
+  // coherence point before it reaches the barrier, after which thread 0 bumps
+  // the arrival counter; the last block reads them with sc1 loads.
   // This is the ordering the ISA gives a wave's memory operations.  The
   // language-level form (release increment, acquire read) was measured: the
   // agent-scope release writes back the whole L2 (buffer_wbl2) and took the
@@ -287,7 +282,7 @@ k_skinny_dual(const f16* __restrict__ A, const uint32_t* __restrict__ B,
               int N, int K, int g, int nrounds) {
   // ROWP: each wave stages its weights through 8 KiB of LDS in the main
   // loop; the block reduction reuses the same memory afterwards.
-  constexpr int RED = (NW - 1) * 16 * 64;
+  constexpr int RED = row_items_lds_floats<1, 1, NW>();
   constexpr int LDSF = ROWP && NW * 2048 > RED ? NW * 2048 : RED;   // floats
   __shared__ __attribute__((aligned(16))) float red[LDSF];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -305,24 +300,22 @@ k_skinny_dual(const f16* __restrict__ A, const uint32_t* __restrict__ B,
   } else
     skinny_wave<INT4, 1, 1, SPW, FL, true, SROW>(A, K, nullptr, 1, M, tl, N, K, g, wave * SPW,
                                                  nrounds, NW * SPW, acc);
-  // Rows 8..15 (lanes q >= 2) hold the second slab's sums: reduce all 16.
-  skinny_block_reduce<1, 1, NW>(red, acc, 16);
-  if (wave != 0) return;
-  // Lane (q, c) with q < 2, c < 8 adds lane (q + 2, c + 8) = lane + 40.
-  f32x4 v[4];
+  // Lanes q >= 2 hold the second slab's sums of the same rows (4*(q & 1) + rr):
+  // items of rows < M are reduced over the waves, then lane (q, c) with
+  // q < 2, c < 8 of the owning wave adds lane (q + 2, c + 8) = lane + 40.
+  constexpr int IPW = row_items_per_wave<1, NW>();
+  f32x4 rv[IPW][1];
+  block_reduce_items<1, 1, NW, true>(red, acc, M, rv);
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
+  for (int k = 0; k < IPW; ++k) {
+    const int rr = wave + k * NW;   // wave-uniform
+    if (rr >= 4 || rr >= M) continue;
+    f32x4 v;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) v[j][r] = acc[0][0][j][r] + __shfl_down(acc[0][0][j][r], 40);
-  if (q >= 2 || c >= 8) return;
-  const int col = n0 + 4 * c;
-  if (col >= N) return;
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int row = 4 * q + r;
-    if (row < M)
-      *(f16x4*)(C + (size_t)row * N + col) =
-          f16x4{(f16)v[0][r], (f16)v[1][r], (f16)v[2][r], (f16)v[3][r]};
+    for (int j = 0; j < 4; ++j) v[j] = rv[k][0][j] + __shfl_down(rv[k][0][j], 40);
+    const int row = 4 * q + rr, col = n0 + 4 * c;
+    if (q < 2 && c < 8 && row < M && col < N)
+      *(f16x4*)(C + (size_t)row * N + col) = f16x4{(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
   }
 }
 

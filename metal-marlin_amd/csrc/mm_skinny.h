@@ -432,6 +432,56 @@ MM_DEV void skinny_block_reduce(float* red, f32x4 (&acc)[MT][NT][4], int mrows) 
   }
 }
 
+// Row-item block reduction.  A row item (mt, rr) of a lane (c, q) is its row
+// 16*mt + 4*q + rr (DUALROWS: the logical row 4*(q & 1) + rr of the two-slab
+// layout, whose lanes q >= 2 hold the second slab) with the four columns
+// 4c + j (j = 0..3) of each tile t as one f32x4.  Every wave parks its items
+// of rows < mrows in LDS (only the rows that are stored move: at one row a
+// quarter of the accumulator), one barrier, then item i is summed over the
+// waves in wave order (the order of skinny_block_reduce, so the sums are the
+// same bits) by wave i % NW.  On return rv[k][t] holds item wave + k*NW of
+// this wave (valid for its lanes whose row is < mrows).
+template <int MT, int NW>
+constexpr int row_items_per_wave() { return (MT * 4 + NW - 1) / NW; }
+template <int MT, int NT, int NW>
+constexpr int row_items_lds_floats() { return NW * MT * 4 * NT * 64 * 4; }
+
+template <int MT, int NT, int NW, bool DUALROWS = false>
+MM_DEV void block_reduce_items(float* red, const f32x4 (&acc)[MT][NT][4], int mrows,
+                               f32x4 (&rv)[row_items_per_wave<MT, NW>()][NT]) {
+  constexpr int NI = MT * 4, IPW = row_items_per_wave<MT, NW>();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, q = lane >> 4;
+  const int qrow = DUALROWS ? 4 * (q & 1) : 4 * q;
+  f32x4* slots = (f32x4*)red;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr)
+      if ((DUALROWS ? 0 : 16 * mt) + qrow + rr < mrows) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+          slots[((wave * NI + mt * 4 + rr) * NT + t) * 64 + lane] =
+              f32x4{acc[mt][t][0][rr], acc[mt][t][1][rr], acc[mt][t][2][rr], acc[mt][t][3][rr]};
+      }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < IPW; ++k) {
+    const int it = wave + k * NW;   // wave-uniform
+    // Items whose lowest row (q = 0) is already past mrows hold nothing.
+    if (it >= NI || (DUALROWS ? 0 : 16 * (it >> 2)) + (it & 3) >= mrows) continue;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      f32x4 part[NW];
+#pragma unroll
+      for (int w = 0; w < NW; ++w) part[w] = slots[((w * NI + it) * NT + t) * 64 + lane];
+      f32x4 v = part[0];
+#pragma unroll
+      for (int w = 1; w < NW; ++w) v += part[w];
+      rv[k][t] = v;
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Column-strip core (M <= 16, g % 32 == 0; no split-K).  The weights are the
 // MFMA A operand and the activations the B operand, so one MFMA 16x16x32
