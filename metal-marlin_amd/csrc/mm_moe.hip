@@ -412,7 +412,7 @@ k_moe_grouped(const f16* __restrict__ X, const int32_t* __restrict__ sorted_idx,
               int N, int g, int act, f16* __restrict__ Y) {
   constexpr int NT = 2;
   constexpr int MOE_NW = NW, MOE_SPW = SPW;
-  __shared__ float red[(MOE_NW - 1) * MT * NT * 16 * 64];
+  __shared__ __attribute__((aligned(16))) float red[row_items_lds_floats<MT, NT, MOE_NW>()];
   const int e = blockIdx.z;
   const int r0 = offsets[e], r1 = offsets[e + 1];
   if (r1 <= r0) return;
@@ -440,38 +440,39 @@ k_moe_grouped(const f16* __restrict__ X, const int32_t* __restrict__ sorted_idx,
     skinny_wave<false, MT, NT, MOE_SPW, FL>(A, K, gather ? sorted_idx + mb : nullptr, topk, mrows,
                                             tl, N, K, g, wave * MOE_SPW, nrounds,
                                             MOE_NW * MOE_SPW, acc);
-    skinny_block_reduce<MT, NT, MOE_NW>(red, acc, mrows);
-    if (wave == 0) {
+    // Row items (mt, rr): lane (c, q) of the owning wave holds row
+    // 16*mt + 4*q + rr, columns 4*c .. 4*c + 3 of both tiles.
+    constexpr int IPW = row_items_per_wave<MT, MOE_NW>();
+    f32x4 rv[IPW][NT];
+    block_reduce_items<MT, NT, MOE_NW>(red, acc, mrows, rv);
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
+    for (int k = 0; k < IPW; ++k) {
+      const int it = wave + k * MOE_NW;
+      const int row = it < MT * 4 ? 16 * (it >> 2) + 4 * q + (it & 3) : mrows;
+      if (row >= mrows) continue;
+      f16* yrow = Y + (size_t)(mb + row) * nout;
+      if (act) {
+        const int col = n0 + 4 * c;
+        if (col < nout) {
+          f16x4 o;
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          const int row = mt * 16 + 4 * q + rr;
-          if (row >= mrows) continue;
-          f16* yrow = Y + (size_t)(mb + row) * nout;
-          if (act) {
-            const int col = n0 + 4 * c;
-            if (col < nout) {
-              f16x4 o;
-#pragma unroll
-              for (int j = 0; j < 4; ++j) {
-                const float gt = acc[mt][0][j][rr], up = acc[mt][1][j][rr];
-                o[j] = (f16)(gt / (1.0f + __expf(-gt)) * up);
-              }
-              *(f16x4*)(yrow + col) = o;
-            }
-          } else {
-#pragma unroll
-            for (int t = 0; t < NT; ++t) {
-              const int col = n0 + t * SK_COLS + 4 * c;
-              if (col < nout)
-                *(f16x4*)(yrow + col) = f16x4{(f16)acc[mt][t][0][rr], (f16)acc[mt][t][1][rr],
-                                              (f16)acc[mt][t][2][rr], (f16)acc[mt][t][3][rr]};
-            }
+          for (int j = 0; j < 4; ++j) {
+            const float gt = rv[k][0][j], up = rv[k][1][j];
+            o[j] = (f16)(gt / (1.0f + __expf(-gt)) * up);
           }
+          *(f16x4*)(yrow + col) = o;
         }
+      } else {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          const int col = n0 + t * SK_COLS + 4 * c;
+          if (col < nout)
+            *(f16x4*)(yrow + col) =
+                f16x4{(f16)rv[k][t][0], (f16)rv[k][t][1], (f16)rv[k][t][2], (f16)rv[k][t][3]};
+        }
+      }
     }
-    __syncthreads();   // wave 0 has read `red` before the next chunk overwrites it
+    __syncthreads();   // every wave has read `red` before the next chunk overwrites it
   }
 }
 

@@ -392,54 +392,14 @@ MM_DEV void skinny_wave(const f16* __restrict__ A, int lda, const int* __restric
   }
 }
 
-// Every wave but wave 0 parks its accumulators in LDS ((NW-1) tiles), one
-// barrier, then wave 0 adds them in wave order (deterministic).  On return
-// wave 0 holds the block sum; the other waves' values are unspecified.
-// Only the lanes that hold rows < mrows move data (lane (c, q) holds rows
-// 16*mt + 4*q .. + 3): at M = 1 that is a quarter of the LDS traffic.
-template <int MT, int NT, int NW>
-MM_DEV void skinny_block_reduce(float* red, f32x4 (&acc)[MT][NT][4], int mrows) {
-  constexpr int TILE = MT * NT * 16 * 64;   // floats per wave: 16 per lane per (mt, t)
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int q = lane >> 4;
-  if (wave > 0) {
-    float* dst = red + (size_t)(wave - 1) * TILE;
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-      if (mt * 16 + 4 * q < mrows) {
-#pragma unroll
-        for (int t = 0; t < NT; ++t)
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-            *(f32x4*)(dst + (((mt * NT + t) * 4 + j) * 64 + lane) * 4) = acc[mt][t][j];
-      }
-  }
-  __syncthreads();
-  if (wave == 0) {
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-      if (mt * 16 + 4 * q < mrows) {
-#pragma unroll
-        for (int w = 0; w < NW - 1; ++w) {
-          const float* src = red + (size_t)w * TILE;
-#pragma unroll
-          for (int t = 0; t < NT; ++t)
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-              acc[mt][t][j] += *(const f32x4*)(src + (((mt * NT + t) * 4 + j) * 64 + lane) * 4);
-        }
-      }
-  }
-}
-
 // Row-item block reduction.  A row item (mt, rr) of a lane (c, q) is its row
 // 16*mt + 4*q + rr (DUALROWS: the logical row 4*(q & 1) + rr of the two-slab
 // layout, whose lanes q >= 2 hold the second slab) with the four columns
 // 4c + j (j = 0..3) of each tile t as one f32x4.  Every wave parks its items
 // of rows < mrows in LDS (only the rows that are stored move: at one row a
 // quarter of the accumulator), one barrier, then item i is summed over the
-// waves in wave order (the order of skinny_block_reduce, so the sums are the
-// same bits) by wave i % NW.  On return rv[k][t] holds item wave + k*NW of
+// waves in wave order (wave 0's value first, then waves 1, 2, ... added one at
+// a time: a fixed order, so the sums are deterministic) by wave i % NW.  On return rv[k][t] holds item wave + k*NW of
 // this wave (valid for its lanes whose row is < mrows).
 template <int MT, int NW>
 constexpr int row_items_per_wave() { return (MT * 4 + NW - 1) / NW; }
