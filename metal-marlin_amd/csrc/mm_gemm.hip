@@ -670,25 +670,45 @@ k_splitk_reduce(const float* __restrict__ part, int ks, int M, int N, f16* __res
 }
 
 // ===========================================================================
-// Host-side planning
+// Host-side planning.  The MM_SK_* / MM_ST_* / MM_PF_* constants are
+// compile-time tunables (overridable with -D for tuning builds).
 // ===========================================================================
+#ifndef MM_SK_NW1
 #define MM_SK_NW1 8         // waves per skinny block, M <= 16 (power of two)
+#endif
+#ifndef MM_SK_NW2
 #define MM_SK_NW2 8         // waves per skinny block, 16 < M <= 32
+#endif
+#ifndef MM_SK_SPW1
 #define MM_SK_SPW1 8        // 32-k steps per wave per round, M <= 16
+#endif
+#ifndef MM_SK_SPW2
 #define MM_SK_SPW2 4        // 32-k steps per wave per round, 16 < M <= 32
-#define MM_SK_KS2 8         // max K split for 16 < M <= 32 (bounds partial traffic;
-                            // 4 -> 8 measured on MI355X: 14336x4096 at M=17/24/32
-                            // 13.9/14.5/15.0 -> 13.2/14.1/14.8 us, others unchanged)
+#endif
+// Max K split for 16 < M <= 32 (bounds partial traffic; 4 -> 8 measured on
+// MI355X: 14336x4096 at M=17/24/32 13.9/14.5/15.0 -> 13.2/14.1/14.8 us,
+// others unchanged).
+#ifndef MM_SK_KS2
+#define MM_SK_KS2 8
+#endif
+#ifndef MM_SK_NOSPLIT_TILES
 #define MM_SK_NOSPLIT_TILES 200   // column tiles from which the K range is not split
+#endif
+#ifndef MM_SK_NOSPLIT_TILES1
 #define MM_SK_NOSPLIT_TILES1 96   // the same for M <= 16
+#endif
+#ifndef MM_SK_MAXBLOCKS
 #define MM_SK_MAXBLOCKS 2048
+#endif
 template <int MT> constexpr int sk_nw() { return MT == 1 ? MM_SK_NW1 : MM_SK_NW2; }
 template <int MT> constexpr int sk_spw() { return MT == 1 ? MM_SK_SPW1 : MM_SK_SPW2; }
 // The Marlin-layout gate/up pair (two column tiles per wave) at M <= 16 takes
 // half-length slabs: twice the blocks along K for the same bytes.  Measured
 // on MI355X, 4096 -> 2 x 14336, M=1: 13.7 -> 13.0 us; M=8 and M=16 within 1%.
 // The row-packed pair keeps 8 steps (4 steps: M=1 16.7 -> 18.5 us).
+#ifndef MM_SK_PAIR_SPW1
 #define MM_SK_PAIR_SPW1 4
+#endif
 template <int MT, int ACT, int ROWP> constexpr int sk_spw_act() {
   return (ACT == SK_SWIGLU || ACT == SK_PAIR) && MT == 1 && ROWP == 0 ? MM_SK_PAIR_SPW1
                                                                       : sk_spw<MT>();
@@ -824,11 +844,17 @@ int launch_skinny_nt2(const f16* A, const uint32_t* B, const f16* S, const f16* 
   return 0;
 }
 
+#ifndef MM_SK_DUAL_NW
 #define MM_SK_DUAL_NW 8
+#endif
 // 64-k steps per wave per round.  Measured at M=1 (qkv / o): 8 waves x 8
 // steps 5.51 / 5.25 us, 8 x 4 5.46 / 5.12, 16 x 4 5.89 / 5.54, 4 x 8
-// 6.12 / 5.79, 4 x 16 5.99 / 5.69.
+// 6.12 / 5.79, 4 x 16 5.99 / 5.69.  With the row-item block reduction:
+// 8 x 8 5.10-5.19 / 4.77-4.84, 16 x 4 5.01-5.03 / 4.65-4.68, 4 x 16
+// 5.82 / 5.45, and the whole layer within run-to-run noise of 8 x 8.
+#ifndef MM_SK_DUAL_SPW
 #define MM_SK_DUAL_SPW MM_SK_SPW1
+#endif
 // The two-slab kernel serves M <= 8 layers whose 64-column plan runs unsplit
 // on fewer than MM_SK_DUAL_BELOW blocks, when 32-column tiles give at least
 // MM_SK_DUAL_MIN_TILES blocks (measured on MI355X at M=1: 4096 -> 6144
@@ -836,8 +862,12 @@ int launch_skinny_nt2(const f16* A, const uint32_t* B, const f16* S, const f16* 
 // slower as 128 unsplit blocks, 9.3 -> 11.1 us, and keeps the split).  Small
 // layers (K*N <= 4096^2) take it even where the 64-column plan would split:
 // 4096 -> 4096 4.9 us against 5.2-5.3 us for the column-strip kernel.
+#ifndef MM_SK_DUAL_BELOW
 #define MM_SK_DUAL_BELOW 128
+#endif
+#ifndef MM_SK_DUAL_MIN_TILES
 #define MM_SK_DUAL_MIN_TILES 96
+#endif
 
 bool use_dual(int M, int N, int K, int g) {
   if (M > 8 || K % 64 != 0 || g % 64 != 0 || N % 4 != 0) return false;
@@ -872,8 +902,12 @@ int launch_dual(const f16* A, const uint32_t* B, const f16* S, const f16* Z, f16
 // picks (measured slower on the others at M=1: 4096x28672 18.7 -> 20.9 us,
 // 14336x4096 12.4 -> 16.7 us).
 
+#ifndef MM_ST_NW
 #define MM_ST_NW 8
+#endif
+#ifndef MM_ST_SPW
 #define MM_ST_SPW 8
+#endif
 
 template <int INT4, int NS>
 int launch_strip(const f16* A, int lda, const uint32_t* B, const f16* S, const f16* Z, f16* C,
@@ -914,7 +948,9 @@ int launch_prefill(const f16* A, int lda, const uint32_t* B, const f16* S, const
 #define PF2_MID 2, 4, 2, 2       // 128 x 256, 8 waves of 64 x 64
 #define PF2_SMALL 1, 4, 2, 2     // 64 x 256, 4 waves of 64 x 64
 
+#ifndef MM_PF_KS_BLOCKS
 #define MM_PF_KS_BLOCKS 200   // split K while the grid has fewer blocks than this
+#endif
 // Prefill plan: tile config (0: 256x256, 1: 128x256, 2: 64x256) and K split.
 struct PrefillPlan {
   int cfg;
