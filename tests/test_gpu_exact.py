@@ -208,6 +208,34 @@ def test_gate_up_pair_bit_exact(rng, M):
     _same(out, ref)
 
 
+@pytest.mark.parametrize("K,N,what", [
+    (4096, 512, "64-column blocks split along K (MT=1 to 16 rows, MT=2 above)"),
+    (2048, 3072, "two-slab to 8 rows, column strips to 16, split MT=2 above"),
+    (256, 25600, "64-column blocks unsplit to 8 rows, 128-column blocks above"),
+])
+def test_decode_every_row_count(rng, K, N, what):
+    """Every M from 1 to 32 on the decode kernels, FP4 and INT4: the block
+    reduction parks only the rows < M of each lane and hands row item
+    (block row 16*mt + 4*q + rr) to wave (4*mt + rr) mod NW, so each row count
+    exercises a different set of owning waves and masked lanes."""
+    import mmfp4
+    g = 128
+    packed, scales = _exact_fp4(rng, K, N, g)
+    up, us, uz = _exact_u4(rng, K, N, g)
+    dp, ds = to_dev(packed), to_dev(scales)
+    dup, dus, duz = to_dev(up), to_dev(us), to_dev(uz)
+    a_all = _acts(rng, 32, K)
+    w = ofp4.dequant_fp4_f32(packed, scales, g)          # gemm_fp4_ref's operand, once
+    wu = ofp4.dequant_u4_f32(up, us, uz, g)
+    for M in range(1, 33):
+        a = a_all[:M]
+        announce(f"exact decode rows M={M} K={K} N={N} ({what})")
+        _same(mmfp4.marlin_gemm_fp4(to_dev(a), dp, ds, g),
+              (a.astype(np.float32) @ w).astype(np.float16))
+        _same(mmfp4.marlin_gemm_int4(to_dev(a), dup, dus, duz, g),
+              (a.astype(np.float32) @ wu).astype(np.float16))
+
+
 @pytest.mark.parametrize("T,k,E,K,N", [(32, 8, 128, 2048, 1536), (32, 8, 128, 768, 2048),
                                        (1024, 8, 128, 2048, 1536), (1024, 8, 128, 768, 2048),
                                        (7, 3, 5, 256, 96)])
