@@ -117,6 +117,9 @@ MM_DEV __amdgpu_buffer_rsrc_t mm_rsrc(const void* base) {
                                            0x00020000);
 }
 constexpr int MM_CPOL_SC1 = 16;
+// A buffer offset past mm_rsrc's range (0x7fffffff bytes): loads return zero
+// and fetch nothing (offsets added to it stay below 2^32).
+constexpr uint32_t MM_DEAD_OFFSET = 0x80000000u;
 MM_DEV f32x4 load_agent_x4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
   return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0,
                                                                          MM_CPOL_SC1));

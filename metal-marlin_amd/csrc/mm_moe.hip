@@ -743,6 +743,10 @@ int grouped_gemm(const uint16_t* X, const int32_t* sorted_idx, const int32_t* of
     MM_CHECK_LAUNCH("mm_moe_grouped_gemm(prefill)");
     return 0;
   }
+  // The decode kernel addresses gathered activation rows with 31-bit byte
+  // offsets (a buffer resource whose out-of-range loads return zero).
+  MM_CHECK_ARG(!gather || (size_t)T * (size_t)K * 2 < ((size_t)1 << 31),
+               "mm_moe_grouped_gemm: gathered activations must be under 2 GiB");
   const int tiles = act ? mm_cdiv(nout, SK_COLS) : mm_cdiv(N, 2 * SK_COLS);
   dim3 grid(tiles, 1, E);
   // Blocks the launch can keep busy: column tiles x experts that can hold a

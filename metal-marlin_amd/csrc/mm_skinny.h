@@ -170,12 +170,17 @@ MM_DEV void skinny_wave(const f16* __restrict__ A, int lda, const int* __restric
   const int KP = K >> 3;
   const int nsteps = (KP + 4 * SLAB - 1) / (4 * SLAB);
 
-  uint32_t aoff[MT];                       // byte offset of A[row][0]
+  // Byte offset of A[row][0] in a buffer resource over A.  Operand rows past
+  // M (the MFMA pads the rows to 16) get an offset past the resource's range,
+  // so their loads return zeros without a memory request: at M = 1 one lane in
+  // 16 fetches activations.
+  const __amdgpu_buffer_rsrc_t ars = mm_rsrc(A);
+  uint32_t aoff[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     const int m = min(mt * 16 + cl, M - 1);
     const int r = rowmap != nullptr ? rowmap[m] / rowdiv : m;
-    aoff[mt] = (uint32_t)r * (uint32_t)lda * 2u;
+    aoff[mt] = mt * 16 + cl < M ? (uint32_t)r * (uint32_t)lda * 2u : MM_DEAD_OFFSET;
   }
   uint32_t coff[NT];                       // column index of this lane's first column
 #pragma unroll
@@ -256,7 +261,8 @@ MM_DEV void skinny_wave(const f16* __restrict__ A, int lda, const int* __restric
       if constexpr (!ASTG) {
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
-          a[i][mt] = *at_bytes<f16x8>(A, aoff[mt] + (uint32_t)kp * 16u);
+          a[i][mt] = __builtin_bit_cast(
+              f16x8, __builtin_amdgcn_raw_buffer_load_b128(ars, aoff[mt] + (uint32_t)kp * 16u, 0, 0));
       }
     }
     if constexpr (RT) {
@@ -471,8 +477,11 @@ MM_DEV void strip_wave(const f16* __restrict__ A, int lda, const int* __restrict
   const int KP = K >> 3;
   const int nsl = (KP + 3) >> 2;
   const int m = min(i, M - 1);
-  const uint32_t aoff = (uint32_t)(rowmap != nullptr ? rowmap[m] / rowdiv : m) *
-                        (uint32_t)lda * 2u;
+  // Operand rows past M fetch nothing (offset past the resource; see skinny_wave).
+  const __amdgpu_buffer_rsrc_t ars = mm_rsrc(A);
+  const uint32_t aoff = i < M ? (uint32_t)(rowmap != nullptr ? rowmap[m] / rowdiv : m) *
+                                    (uint32_t)lda * 2u
+                              : MM_DEAD_OFFSET;
   uint32_t bcol[NS], scol[NS];
 #pragma unroll
   for (int t = 0; t < NS; ++t) {
@@ -506,7 +515,8 @@ MM_DEV void strip_wave(const f16* __restrict__ A, int lda, const int* __restrict
       for (int t = 0; t < NS; ++t)
         R.w[u][t] = __builtin_nontemporal_load(
             at_bytes<uint32_t>(B, ((uint32_t)kp * (uint32_t)N + bcol[t]) * 4u));
-      R.a[u] = *at_bytes<f16x8>(A, aoff + (uint32_t)kp * 16u);
+      R.a[u] = __builtin_bit_cast(
+          f16x8, __builtin_amdgcn_raw_buffer_load_b128(ars, aoff + (uint32_t)kp * 16u, 0, 0));
     }
   };
   auto math = [&](int r, StripRound<NS, SPW, NF>& R) {
