@@ -241,7 +241,10 @@ int mm_softmax_topk(const void* logits, int logits_f32, int T, int E, int k, int
  * N/2 columns are gate and the last N/2 up, Y[r, j] = silu(gate_j) * up_j is
  * [T*k, N/2].  Replaces metal_marlin/kernels/moe.py:583-727
  * (moe_expert_gemm_fp4, kernel src/moe_expert_gemm.metal:557-782) and the
- * expert MLP of metal_marlin/moe_dispatch.py:1241-1431 (_fused_expert_mlp). */
+ * expert MLP of metal_marlin/moe_dispatch.py:1241-1431 (_fused_expert_mlp).
+ * Status 1 when one expert's packed weights reach 4 GiB, or when gather != 0,
+ * the groups are decode-sized (at most 24 rows per expert on average) and X
+ * (T rows of K halves) reaches 2 GiB. */
 int mm_moe_grouped_gemm(const uint16_t* X, const int32_t* sorted_idx, const int32_t* offsets,
                         int gather, int k, int T, const uint32_t* B, const uint16_t* S, int E,
                         int K, int N, int group_size, int act, uint16_t* Y, void* stream);
