@@ -208,18 +208,19 @@ def test_gate_up_pair_bit_exact(rng, M):
     _same(out, ref)
 
 
+@pytest.mark.parametrize("g", [32, 128])
 @pytest.mark.parametrize("K,N,what", [
     (4096, 512, "64-column blocks split along K (MT=1 to 16 rows, MT=2 above)"),
     (2048, 3072, "two-slab to 8 rows, column strips to 16, split MT=2 above"),
     (256, 25600, "64-column blocks unsplit to 8 rows, 128-column blocks above"),
 ])
-def test_decode_every_row_count(rng, K, N, what):
+def test_decode_every_row_count(rng, K, N, what, g):
     """Every M from 1 to 32 on the decode kernels, FP4 and INT4: the block
     reduction parks only the rows < M of each lane and hands row item
     (block row 16*mt + 4*q + rr) to wave (4*mt + rr) mod NW, so each row count
-    exercises a different set of owning waves and masked lanes."""
+    exercises a different set of owning waves and masked lanes; g = 32 flushes
+    the group scale every 32-k step, g = 128 every fourth."""
     import mmfp4
-    g = 128
     packed, scales = _exact_fp4(rng, K, N, g)
     up, us, uz = _exact_u4(rng, K, N, g)
     dp, ds = to_dev(packed), to_dev(scales)
@@ -229,7 +230,7 @@ def test_decode_every_row_count(rng, K, N, what):
     wu = ofp4.dequant_u4_f32(up, us, uz, g)
     for M in range(1, 33):
         a = a_all[:M]
-        announce(f"exact decode rows M={M} K={K} N={N} ({what})")
+        announce(f"exact decode rows M={M} K={K} N={N} g={g} ({what})")
         _same(mmfp4.marlin_gemm_fp4(to_dev(a), dp, ds, g),
               (a.astype(np.float32) @ w).astype(np.float16))
         _same(mmfp4.marlin_gemm_int4(to_dev(a), dup, dus, duz, g),
