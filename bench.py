@@ -671,6 +671,9 @@ def main() -> int:
                     default="all",
                     help="run one workload alone (for profiling); the default runs all and "
                          "prints the contract line")
+    ap.add_argument("--layer-m", type=int, default=1,
+                    help="rows of the layer GEMMs for --section layer (1: the metric's "
+                         "workload; 8, 16, 32: the other decode sizes of config 2 and 3)")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="no timing: run a 512 MiB copy (counter calibration) then the M=1 layer "
                          "GEMMs and the M=2048 prefill GEMMs, for rocprofv3 --pmc runs")
@@ -693,7 +696,7 @@ def main() -> int:
     if args.section != "all":
         # One workload alone, for a clean rocprofv3 kernel trace of it.
         if args.section == "layer":
-            r = run_layer_bench(torch, mmfp4, 1, args.steps, args.warmup)
+            r = run_layer_bench(torch, mmfp4, args.layer_m, args.steps, args.warmup)
             res = {"us_per_step": round(1e3 * r["ms_per_step"], 3), "per_shape": r["per_shape"],
                    "TBps": round(r["step_bytes"] / (r["ms_per_step"] * 1e-3) / 1e12, 4)}
         elif args.section == "prefill":
