@@ -404,9 +404,10 @@ MM_DEV void skinny_wave(const f16* __restrict__ A, int lda, const int* __restric
 // 4c + j (j = 0..3) of each tile t as one f32x4.  Every wave parks its items
 // of rows < mrows in LDS (only the rows that are stored move: at one row a
 // quarter of the accumulator), one barrier, then item i is summed over the
-// waves in wave order (wave 0's value first, then waves 1, 2, ... added one at
-// a time: a fixed order, so the sums are deterministic) by wave i % NW.  On return rv[k][t] holds item wave + k*NW of
-// this wave (valid for its lanes whose row is < mrows).
+// waves by wave i % NW, in wave order (wave 0's value first, then waves 1, 2,
+// ... added one at a time: a fixed order, so the sums are deterministic).  On
+// return rv[k][t] holds item wave + k*NW of this wave (valid for its lanes
+// whose row is < mrows).
 template <int MT, int NW>
 constexpr int row_items_per_wave() { return (MT * 4 + NW - 1) / NW; }
 template <int MT, int NT, int NW>
