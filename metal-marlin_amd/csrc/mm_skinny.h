@@ -261,8 +261,8 @@ MM_DEV void skinny_wave(const f16* __restrict__ A, int lda, const int* __restric
       if constexpr (!ASTG) {
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
-          a[i][mt] = __builtin_bit_cast(
-              f16x8, __builtin_amdgcn_raw_buffer_load_b128(ars, aoff[mt] + (uint32_t)kp * 16u, 0, 0));
+          a[i][mt] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(
+                                                  ars, aoff[mt] + (uint32_t)kp * 16u, 0, 0));
       }
     }
     if constexpr (RT) {
